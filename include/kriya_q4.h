@@ -1,0 +1,141 @@
+/*
+ * kriya_q4.h — C ABI of the MI355X (gfx950) Q4_G64 matmul path.
+ *
+ * Drop-in boundary for kriya-rt's Q4 operator surface
+ * (crates/kriya-backend-metal/src/encoder.rs, MetalExecutor::encode_q4_*).
+ * Each entry point names the reference function it replaces.
+ *
+ * Conventions
+ *   - The caller owns all device memory.  Pointers are device pointers unless
+ *     a comment says otherwise.  No entry point allocates device memory.
+ *   - Calls enqueue work on `stream` (a hipStream_t; NULL = the null stream)
+ *     and return at once.  0 on success, a negative KR_E* code on failure;
+ *     kr_last_error() returns the message (thread-local).
+ *   - Shapes and alignment are checked on the host before any launch; a call
+ *     that fails a check enqueues nothing.  (The reference performs no shape
+ *     checks in its encode functions, encoder.rs:2361-2536.)
+ *   - Calls on distinct streams are independent; the library keeps no
+ *     per-call state on the device.
+ *   - Results do not depend on the launch grid: every output element is
+ *     reduced by one wavefront in a fixed order (no atomics on data).
+ *
+ * Weight format (kr_q4_matrix): the planar affine Q4_G64 triplet
+ *   qw     u32  [n, k/8]   word w of row r holds elements 8w..8w+7 of that
+ *                          row, element 8w+j in bits 4j..4j+3
+ *   scales bf16 [n, k/64]  raw bits
+ *   biases bf16 [n, k/64]  raw bits
+ *   w[r, c] = fma(q, scale, bias)            (quantizer.rs:112-126)
+ * Its nibble plane is byte-identical to the `qs` bytes of kriya's 36-byte
+ * BlockQ4Group64 (tensor.rs:104-115): kr_q4_from_blocks36() converts.
+ */
+#ifndef KRIYA_Q4_H
+#define KRIYA_Q4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KR_ABI_VERSION 1
+
+/* ---- error codes ---- */
+#define KR_OK 0
+#define KR_E_INVALID (-1)     /* null pointer, bad enum, bad count            */
+#define KR_E_SHAPE (-2)       /* k % 64 != 0, mismatched matrices, too large  */
+#define KR_E_ALIGN (-3)       /* a pointer is not aligned as documented        */
+#define KR_E_HIP (-4)         /* the HIP runtime reported an error             */
+#define KR_E_WORKSPACE (-5)   /* workspace missing or smaller than required    */
+#define KR_E_UNSUPPORTED (-6) /* no kernel for this combination                */
+
+/* ---- element types of activations / outputs ---- */
+#define KR_DTYPE_BF16 0
+#define KR_DTYPE_F32 1
+
+/* ---- gated activations (descriptor.rs ActivationVariant; encoder.rs:2718-2722) ---- */
+#define KR_ACT_SWIGLU 0 /* silu(g) * u                      */
+#define KR_ACT_GEGLU 1  /* gelu_tanh(g) * u                 */
+#define KR_ACT_RELU 2   /* max(g, 0) * u                    */
+
+typedef struct kr_q4_matrix {
+    const uint32_t *qw;     /* [n, k/8], 16-byte aligned            */
+    const uint16_t *scales; /* [n, k/64] bf16 bits, 2-byte aligned  */
+    const uint16_t *biases; /* [n, k/64] bf16 bits, 2-byte aligned  */
+    uint32_t n;             /* rows = output features               */
+    uint32_t k;             /* columns = input features, k % 64 == 0 */
+} kr_q4_matrix;
+
+/* ---- library ---- */
+int kr_abi_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char *kr_last_error(void);
+
+/* Process-wide launch tuning (no counterpart in the reference, whose launch
+ * shapes are fixed in encoder.rs).  Not synchronised with calls in flight on
+ * other threads.  Results never depend on these values. */
+#define KR_OPT_GEMV_ROWS_PER_WAVE 1 /* 1, 2, 4 (default) or 8                  */
+#define KR_OPT_GEMV_MAX_BLOCKS 2    /* 0 (default): one pass; > 0: grid-stride */
+int kr_set_option(int option, int value);
+int kr_get_option(int option);
+
+/* ---- format boundary ---- */
+
+/* Bit-exact dequantisation: out[r, c] = fma(q, scale, bias) as f32 [n, k].
+ * Replaces dequantize_q4_group64_to_f32 (crates/kriya-core/src/quantizer.rs:112-126)
+ * for on-device checks.  out 16-byte aligned. */
+int kr_q4_dequant(const kr_q4_matrix *w, float *out, void *stream);
+
+/* 36-byte BlockQ4Group64 blocks [n, k/64] (tensor.rs:104-115; block (r, g) at
+ * index r*(k/64)+g, q4_gemm_and_moe.metal:951) -> planar triplet.  The nibble
+ * bytes are copied verbatim.  blocks 4-byte aligned, qw 16-byte aligned.
+ * Replaces the bind-time repack of encoder.rs:651-703 / safetensors_loader.rs:221-273. */
+int kr_q4_from_blocks36(const void *blocks, uint32_t n, uint32_t k,
+                        uint32_t *qw, uint16_t *scales, uint16_t *biases, void *stream);
+/* Planar triplet -> 36-byte blocks (inverse of the above, byte-identical). */
+int kr_q4_to_blocks36(const kr_q4_matrix *w, void *blocks, void *stream);
+
+/* MLX scale/bias planes stored as IEEE half -> bf16 bits, element-wise:
+ * bf16_rne(f16_to_f32(h)).  Replaces parse_half_endian(is_f16 = true)
+ * (safetensors_loader.rs:310-318; quantizer.rs:19-57).  in may equal out. */
+int kr_f16_to_bf16(const uint16_t *in, uint16_t *out, size_t count, void *stream);
+
+/* ---- Q4 linear: encoder.rs:2361-2420 (encode_q4_linear) and
+ *      encoder.rs:2497-2536 (encode_q4_linear_accumulate) ----
+ * y[i, r] = sum_c x[i, c] * w[r, c] for i < m, accumulated in f32.
+ *   x: bf16 [m, w->k], 16-byte aligned (the reference's input_byte_offset is
+ *      folded into the pointer by the caller).
+ *   y: [m, w->n] of y_dtype.
+ *   accumulate = 0: y = result (bf16 outputs are RNE of the f32 result).
+ *   accumulate = 1: y = y + result, in place; for KR_DTYPE_BF16 the stored
+ *      value is bf16(f32(y) + result) (q4_gemm_and_moe.metal:1407-1420).
+ * m == 1 runs the decode GEMV; m > 1 runs the batched kernels. */
+int kr_q4_linear(const kr_q4_matrix *w, const uint16_t *x, uint32_t m,
+                 void *y, int y_dtype, int accumulate, void *stream);
+
+/* ---- fused gate+up+activation: encoder.rs:2703-2848 (encode_fused_gate_up) ----
+ * a[i, j] = act(gate_j . x_i) * (up_j . x_i) for j < gate->n, both dots in f32.
+ *   gate, up: same n (intermediate) and k (hidden).
+ *   act_out: [m, gate->n] of act_dtype (bf16 = RNE of the f32 value, as the
+ *   reference kernels store it, q4_gemm_and_moe.metal:2076). */
+int kr_q4_gate_up_act(const kr_q4_matrix *gate, const kr_q4_matrix *up,
+                      const uint16_t *x, uint32_t m, void *act_out, int act_dtype,
+                      int activation, void *stream);
+
+/* ---- dense MLP: encoder.rs:2851-2906 (encode_dense_mlp) ----
+ * h[i, :] += down . bf16(act(gate . h_i) * (up . h_i))   for i < m
+ * The residual h is read as bf16 and updated in place (h_dtype bf16: stored
+ * RNE of f32(h) + f32 sum; f32: f32 += sum).  The MLP input is the bf16 view
+ * of h; for h_dtype f32 a separate bf16 input x must be given (x may be NULL
+ * when h_dtype is bf16, then x = h).  The intermediate activation is kept in
+ * bf16 in the workspace, as the reference stores it.
+ * workspace: device memory of at least kr_q4_mlp_workspace_bytes(m, gate->n). */
+size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t intermediate);
+int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down,
+              const uint16_t *x, void *h, int h_dtype, uint32_t m, int activation,
+              void *workspace, size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KRIYA_Q4_H */

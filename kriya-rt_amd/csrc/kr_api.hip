@@ -1,0 +1,211 @@
+// kr_api.hip — the C ABI (include/kriya_q4.h): argument validation, dispatch
+// policy and error reporting.  Mirrors the operator surface of
+// crates/kriya-backend-metal/src/encoder.rs (encode_q4_linear :2361-2420,
+// encode_q4_linear_accumulate :2497-2536, encode_fused_gate_up :2703-2848,
+// encode_dense_mlp :2851-2906), with the shape checks the reference lacks.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "kriya_q4.h"
+#include "kr_internal.hpp"
+
+namespace kr {
+
+Tuning &tuning() {
+    static Tuning t;
+    return t;
+}
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int ok() {
+    g_err.clear();
+    return KR_OK;
+}
+
+int hip_status(hipError_t e, const char *what) {
+    if (e != hipSuccess) return fail(KR_E_HIP, "%s: %s", what, hipGetErrorString(e));
+    return ok();
+}
+
+bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_matrix(const kr_q4_matrix *w, const char *name) {
+    if (!w) return fail(KR_E_INVALID, "%s: matrix descriptor is NULL", name);
+    if (!w->qw || !w->scales || !w->biases) return fail(KR_E_INVALID, "%s: qw/scales/biases must be non-NULL", name);
+    if (w->k == 0 || w->k % 64 != 0) return fail(KR_E_SHAPE, "%s: k=%u is not a positive multiple of 64", name, w->k);
+    if (w->n == 0) return fail(KR_E_SHAPE, "%s: n must be positive", name);
+    if (!aligned(w->qw, 16)) return fail(KR_E_ALIGN, "%s: qw must be 16-byte aligned", name);
+    if (!aligned(w->scales, 2) || !aligned(w->biases, 2))
+        return fail(KR_E_ALIGN, "%s: scales/biases must be 2-byte aligned", name);
+    if ((uint64_t)w->n * (w->k / 8) > (1ull << 40)) return fail(KR_E_SHAPE, "%s: matrix too large", name);
+    return KR_OK;
+}
+
+Q4Mat to_mat(const kr_q4_matrix *w) { return Q4Mat{w->qw, w->scales, w->biases, w->n, w->k}; }
+
+size_t dtype_size(int dt) { return dt == KR_DTYPE_F32 ? 4 : 2; }
+
+bool valid_dtype(int dt) { return dt == KR_DTYPE_BF16 || dt == KR_DTYPE_F32; }
+bool valid_act(int a) { return a == KR_ACT_SWIGLU || a == KR_ACT_GEGLU || a == KR_ACT_RELU; }
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+}  // namespace kr
+
+using namespace kr;
+
+extern "C" {
+
+int kr_abi_version(void) { return KR_ABI_VERSION; }
+
+const char *kr_last_error(void) { return g_err.c_str(); }
+
+int kr_set_option(int option, int value) {
+    switch (option) {
+        case KR_OPT_GEMV_ROWS_PER_WAVE:
+            if (value != 1 && value != 2 && value != 4 && value != 8)
+                return fail(KR_E_INVALID, "rows per wave must be 1, 2, 4 or 8");
+            tuning().gemv_rows_per_wave = value;
+            return ok();
+        case KR_OPT_GEMV_MAX_BLOCKS:
+            if (value < 0) return fail(KR_E_INVALID, "max blocks must be >= 0");
+            tuning().gemv_max_blocks = value;
+            return ok();
+        default: return fail(KR_E_INVALID, "unknown option %d", option);
+    }
+}
+
+int kr_get_option(int option) {
+    switch (option) {
+        case KR_OPT_GEMV_ROWS_PER_WAVE: return tuning().gemv_rows_per_wave;
+        case KR_OPT_GEMV_MAX_BLOCKS: return tuning().gemv_max_blocks;
+        default: return fail(KR_E_INVALID, "unknown option %d", option);
+    }
+}
+
+int kr_q4_dequant(const kr_q4_matrix *w, float *out, void *stream) {
+    if (int rc = check_matrix(w, "w")) return rc;
+    if (!out) return fail(KR_E_INVALID, "out is NULL");
+    if (!aligned(out, 16)) return fail(KR_E_ALIGN, "out must be 16-byte aligned");
+    return hip_status(launch_format_dequant(to_mat(w), out, (hipStream_t)stream), "kr_q4_dequant");
+}
+
+int kr_q4_from_blocks36(const void *blocks, uint32_t n, uint32_t k, uint32_t *qw, uint16_t *scales,
+                        uint16_t *biases, void *stream) {
+    if (!blocks || !qw || !scales || !biases) return fail(KR_E_INVALID, "NULL pointer");
+    if (k == 0 || k % 64 != 0) return fail(KR_E_SHAPE, "k=%u is not a positive multiple of 64", k);
+    if (!aligned(blocks, 4)) return fail(KR_E_ALIGN, "blocks must be 4-byte aligned");
+    if (!aligned(qw, 16)) return fail(KR_E_ALIGN, "qw must be 16-byte aligned");
+    if (!aligned(scales, 2) || !aligned(biases, 2)) return fail(KR_E_ALIGN, "scales/biases must be 2-byte aligned");
+    return hip_status(launch_from_blocks36(blocks, n, k, qw, scales, biases, (hipStream_t)stream),
+                      "kr_q4_from_blocks36");
+}
+
+int kr_q4_to_blocks36(const kr_q4_matrix *w, void *blocks, void *stream) {
+    if (int rc = check_matrix(w, "w")) return rc;
+    if (!blocks) return fail(KR_E_INVALID, "blocks is NULL");
+    if (!aligned(blocks, 4)) return fail(KR_E_ALIGN, "blocks must be 4-byte aligned");
+    return hip_status(launch_to_blocks36(to_mat(w), blocks, (hipStream_t)stream), "kr_q4_to_blocks36");
+}
+
+int kr_f16_to_bf16(const uint16_t *in, uint16_t *out, size_t count, void *stream) {
+    if (count == 0) return ok();
+    if (!in || !out) return fail(KR_E_INVALID, "NULL pointer");
+    if (!aligned(in, 2) || !aligned(out, 2)) return fail(KR_E_ALIGN, "in/out must be 2-byte aligned");
+    return hip_status(launch_f16_to_bf16(in, out, count, (hipStream_t)stream), "kr_f16_to_bf16");
+}
+
+int kr_q4_linear(const kr_q4_matrix *w, const uint16_t *x, uint32_t m, void *y, int y_dtype, int accumulate,
+                 void *stream) {
+    if (int rc = check_matrix(w, "w")) return rc;
+    if (!valid_dtype(y_dtype)) return fail(KR_E_INVALID, "y_dtype %d is not KR_DTYPE_BF16/F32", y_dtype);
+    if (accumulate != 0 && accumulate != 1) return fail(KR_E_INVALID, "accumulate must be 0 or 1");
+    if (m == 0) return ok();
+    if (!x || !y) return fail(KR_E_INVALID, "x/y must be non-NULL");
+    if (!aligned(x, 16)) return fail(KR_E_ALIGN, "x must be 16-byte aligned");
+    if (!aligned(y, dtype_size(y_dtype))) return fail(KR_E_ALIGN, "y is misaligned for its dtype");
+    const Q4Mat a = to_mat(w);
+    const int epi = accumulate ? (y_dtype == KR_DTYPE_F32 ? kAccF32 : kAccBF16)
+                               : (y_dtype == KR_DTYPE_F32 ? kStoreF32 : kStoreBF16);
+    hipStream_t s = (hipStream_t)stream;
+    const size_t ysz = dtype_size(y_dtype);
+    for (uint32_t i = 0; i < m; ++i) {
+        hipError_t e = launch_gemv(a, nullptr, x + (size_t)i * w->k, (char *)y + (size_t)i * w->n * ysz, epi, 0, s);
+        if (e != hipSuccess) return hip_status(e, "kr_q4_linear");
+    }
+    return ok();
+}
+
+int kr_q4_gate_up_act(const kr_q4_matrix *gate, const kr_q4_matrix *up, const uint16_t *x, uint32_t m,
+                      void *act_out, int act_dtype, int activation, void *stream) {
+    if (int rc = check_matrix(gate, "gate")) return rc;
+    if (int rc = check_matrix(up, "up")) return rc;
+    if (gate->n != up->n || gate->k != up->k)
+        return fail(KR_E_SHAPE, "gate [%u,%u] and up [%u,%u] differ", gate->n, gate->k, up->n, up->k);
+    if (!valid_dtype(act_dtype)) return fail(KR_E_INVALID, "act_dtype %d invalid", act_dtype);
+    if (!valid_act(activation)) return fail(KR_E_INVALID, "activation %d invalid", activation);
+    if (m == 0) return ok();
+    if (!x || !act_out) return fail(KR_E_INVALID, "x/act_out must be non-NULL");
+    if (!aligned(x, 16)) return fail(KR_E_ALIGN, "x must be 16-byte aligned");
+    if (!aligned(act_out, dtype_size(act_dtype))) return fail(KR_E_ALIGN, "act_out misaligned");
+    const Q4Mat g = to_mat(gate), u = to_mat(up);
+    const int epi = act_dtype == KR_DTYPE_F32 ? kGateUpF32 : kGateUpBF16;
+    hipStream_t s = (hipStream_t)stream;
+    const size_t osz = dtype_size(act_dtype);
+    for (uint32_t i = 0; i < m; ++i) {
+        hipError_t e = launch_gemv(g, &u, x + (size_t)i * gate->k, (char *)act_out + (size_t)i * gate->n * osz, epi,
+                                   activation, s);
+        if (e != hipSuccess) return hip_status(e, "kr_q4_gate_up_act");
+    }
+    return ok();
+}
+
+size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t intermediate) {
+    return round_up((size_t)m * intermediate * 2, 256);
+}
+
+int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, const uint16_t *x,
+              void *h, int h_dtype, uint32_t m, int activation, void *workspace, size_t workspace_bytes,
+              void *stream) {
+    if (int rc = check_matrix(gate, "gate")) return rc;
+    if (int rc = check_matrix(up, "up")) return rc;
+    if (int rc = check_matrix(down, "down")) return rc;
+    if (gate->n != up->n || gate->k != up->k) return fail(KR_E_SHAPE, "gate and up shapes differ");
+    if (down->k != gate->n || down->n != gate->k)
+        return fail(KR_E_SHAPE, "down [%u,%u] does not match gate/up [%u,%u]", down->n, down->k, gate->n, gate->k);
+    if (!valid_dtype(h_dtype)) return fail(KR_E_INVALID, "h_dtype %d invalid", h_dtype);
+    if (!valid_act(activation)) return fail(KR_E_INVALID, "activation %d invalid", activation);
+    if (m == 0) return ok();
+    if (!h) return fail(KR_E_INVALID, "h is NULL");
+    if (!x) {
+        if (h_dtype != KR_DTYPE_BF16) return fail(KR_E_INVALID, "x is required when h is f32");
+        x = (const uint16_t *)h;
+    }
+    if (!aligned(x, 16)) return fail(KR_E_ALIGN, "x must be 16-byte aligned");
+    if (!aligned(h, dtype_size(h_dtype))) return fail(KR_E_ALIGN, "h misaligned");
+    const size_t need = kr_q4_mlp_workspace_bytes(m, gate->n);
+    if (!workspace || workspace_bytes < need)
+        return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
+    uint16_t *act = (uint16_t *)workspace;
+    if (int rc = kr_q4_gate_up_act(gate, up, x, m, act, KR_DTYPE_BF16, activation, stream)) return rc;
+    return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,110 @@
+// kr_device.hpp — gfx950 device helpers shared by the Q4_G64 kernels.
+//
+// Data layout (planar affine Q4_G64, the C ABI's kr_q4_matrix):
+//   qw     u32 [n, k/8]   element 8w+j of a row in bits 4j..4j+3 of word w
+//   scales bf16 [n, k/64], biases bf16 [n, k/64]
+//   w = fma(q, scale, bias)   (crates/kriya-core/src/quantizer.rs:112-126)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kr {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+struct Q4Mat {
+    const uint32_t *qw;
+    const uint16_t *sc;
+    const uint16_t *bi;
+    uint32_t n, k;
+};
+
+// ---- bf16 <-> f32 (quantizer.rs:19-29: RNE with a wrapping add, exact widening)
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16(float v) {
+    uint32_t u = __float_as_uint(v);
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// ---- nibble unpack without conversion instructions.
+// For j in 0..3, bits 4j..4j+3 and 16+4j..16+4j+3 of w (elements j and j+4 of
+// the word) are placed under the bf16 pattern 0x4300 (= 128.0, ulp 1), giving
+// the exact bf16 pair (128 + q_j, 128 + q_{j+4}).  The affine map is then
+// applied per group: sum w*x = s * sum (128+q) x + (b - 128 s) * sum x.
+__device__ __forceinline__ uint32_t q4_pair_bf16(uint32_t w, int j) {
+    return ((w >> (4 * j)) & 0x000F000Fu) | 0x43004300u;
+}
+
+// Same with the f16 pattern 0x6400 (= 1024.0, ulp 1): exact (1024 + q) halves.
+__device__ __forceinline__ uint32_t q4_pair_f16(uint32_t w, int j) {
+    return ((w >> (4 * j)) & 0x000F000Fu) | 0x64006400u;
+}
+
+// v_dot2_f32_bf16: a.lo*b.lo + a.hi*b.hi + c in f32.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b),
+                                           c, false);
+}
+
+// (a.lo16, b.lo16) and (a.hi16, b.hi16): pairs x_{i}, x_{i+4} from words (x_i, x_{i+1}), (x_{i+4}, x_{i+5}).
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) { return (a & 0xFFFFu) | (b << 16); }
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xFFFF0000u); }
+
+// ---- loads that do not keep streamed weights in the caches
+template <typename T>
+__device__ __forceinline__ T ld_stream(const T *p) {
+    return __builtin_nontemporal_load(p);
+}
+
+// ---- gated activations (q4_gemm_and_moe.metal:2064-2071)
+__device__ __forceinline__ float activation(float g, int variant) {
+    if (variant == 0) return g / (1.0f + expf(-g));
+    if (variant == 1) {
+        const float kSqrt2OverPi = 0.7978845608f;
+        float cubic = fmaf(0.044715f * g, g * g, g);
+        return 0.5f * g * (1.0f + tanhf(kSqrt2OverPi * cubic));
+    }
+    return fmaxf(g, 0.0f);
+}
+
+// ---- wavefront reductions (64 lanes)
+// Reduces R per-lane values at once.  The first log2(R) butterfly steps swap
+// halves of the value set between lane pairs, so each step moves R/2, R/4, ...
+// values instead of R; afterwards every lane of the 64/R-lane segment s holds
+// the total of value s.  Fixed order: the result is identical on every launch.
+template <int R>
+__device__ __forceinline__ float wave_reduce_rows(float (&v)[R], int lane) {
+#pragma unroll
+    for (int half = R / 2, mask = 32; half >= 1; half >>= 1, mask >>= 1) {
+        const bool upper = (lane & mask) != 0;
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            float send = upper ? v[i] : v[i + half];
+            float keep = upper ? v[i + half] : v[i];
+            v[i] = keep + __shfl_xor(send, mask);
+        }
+    }
+    float s = v[0];
+#pragma unroll
+    for (int mask = 32 / R; mask >= 1; mask >>= 1) s += __shfl_xor(s, mask);
+    return s;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) v += __shfl_xor(v, mask);
+    return v;
+}
+
+}  // namespace kr

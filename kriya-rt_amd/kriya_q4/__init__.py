@@ -1,0 +1,254 @@
+"""Python binding of libkriya_q4.so (the C ABI in include/kriya_q4.h).
+
+Device memory and streams come from PyTorch (plumbing only): every call passes
+raw device pointers and the current HIP stream to the C ABI, which launches
+the gfx950 kernels.  There is no fallback: if the library is missing or no GPU
+is present, calls raise.
+
+Names mirror kriya-rt's operator surface (crates/kriya-backend-metal/src/
+encoder.rs): ``encode_q4_linear`` (:2361), ``encode_q4_linear_accumulate``
+(:2497), ``encode_fused_gate_up`` (:2703), ``encode_dense_mlp`` (:2851).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from typing import Optional
+
+import numpy as np
+import torch  # must be imported before the library: it loads the HIP runtime both share
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_DIR, "libkriya_q4.so")
+
+# C ABI constants (include/kriya_q4.h)
+KR_OK = 0
+KR_E_INVALID, KR_E_SHAPE, KR_E_ALIGN, KR_E_HIP, KR_E_WORKSPACE, KR_E_UNSUPPORTED = -1, -2, -3, -4, -5, -6
+DTYPE_BF16, DTYPE_F32 = 0, 1
+ACT_SWIGLU, ACT_GEGLU, ACT_RELU = 0, 1, 2
+OPT_GEMV_ROWS_PER_WAVE, OPT_GEMV_MAX_BLOCKS = 1, 2
+
+_lib = None
+
+
+class KrError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"kriya_q4 error {code}: {msg}")
+        self.code = code
+
+
+class kr_q4_matrix(ctypes.Structure):
+    _fields_ = [("qw", ctypes.c_void_p), ("scales", ctypes.c_void_p), ("biases", ctypes.c_void_p),
+                ("n", ctypes.c_uint32), ("k", ctypes.c_uint32)]
+
+
+def build() -> None:
+    """Compile libkriya_q4.so with hipcc for gfx950 (in-tree)."""
+    subprocess.run(["make", "-s", "-C", _PKG_DIR, f"-j{min(os.cpu_count() or 1, 16)}"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        L = ctypes.CDLL(LIB_PATH)
+        M = ctypes.POINTER(kr_q4_matrix)
+        vp, u32, i32, sz = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_int, ctypes.c_size_t
+        sig = {
+            "kr_abi_version": (i32, []),
+            "kr_last_error": (ctypes.c_char_p, []),
+            "kr_set_option": (i32, [i32, i32]),
+            "kr_get_option": (i32, [i32]),
+            "kr_q4_dequant": (i32, [M, vp, vp]),
+            "kr_q4_from_blocks36": (i32, [vp, u32, u32, vp, vp, vp, vp]),
+            "kr_q4_to_blocks36": (i32, [M, vp, vp]),
+            "kr_f16_to_bf16": (i32, [vp, vp, sz, vp]),
+            "kr_q4_linear": (i32, [M, vp, u32, vp, i32, i32, vp]),
+            "kr_q4_gate_up_act": (i32, [M, M, vp, u32, vp, i32, i32, vp]),
+            "kr_q4_mlp_workspace_bytes": (sz, [u32, u32]),
+            "kr_q4_mlp": (i32, [M, M, M, vp, vp, i32, u32, i32, vp, sz, vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != KR_OK:
+        raise KrError(rc, lib().kr_last_error().decode())
+
+
+def _stream(stream) -> Optional[int]:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("tensor must be on the GPU")
+    return t.data_ptr()
+
+
+def set_option(option: int, value: int) -> None:
+    _check(lib().kr_set_option(option, value))
+
+
+def get_option(option: int) -> int:
+    return int(lib().kr_get_option(option))
+
+
+class Q4Matrix:
+    """Planar Q4_G64 weights resident on the GPU.
+
+    qw int32 [n, k/8] (u32 bits), scales/biases int16 [n, k/64] (bf16 bits).
+    """
+
+    def __init__(self, qw: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor):
+        self.qw, self.scales, self.biases = qw, scales, biases
+        self.n = int(qw.shape[0])
+        self.k = int(qw.shape[1]) * 8
+        self._desc = kr_q4_matrix(qw.data_ptr(), scales.data_ptr(), biases.data_ptr(), self.n, self.k)
+
+    @classmethod
+    def from_numpy(cls, qw: np.ndarray, scales: np.ndarray, biases: np.ndarray, device="cuda") -> "Q4Matrix":
+        def up(a, dt):
+            return torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(device)
+        return cls(up(qw, np.int32), up(scales, np.int16), up(biases, np.int16))
+
+    @classmethod
+    def empty(cls, n: int, k: int, device="cuda") -> "Q4Matrix":
+        return cls(torch.empty((n, k // 8), dtype=torch.int32, device=device),
+                   torch.empty((n, k // 64), dtype=torch.int16, device=device),
+                   torch.empty((n, k // 64), dtype=torch.int16, device=device))
+
+    @classmethod
+    def from_blocks36(cls, blocks: torch.Tensor, n: int, k: int, stream=None) -> "Q4Matrix":
+        """36-byte BlockQ4Group64 blocks (uint8 device tensor) -> planar, on the GPU."""
+        w = cls.empty(n, k, device=blocks.device)
+        _check(lib().kr_q4_from_blocks36(_ptr(blocks), n, k, _ptr(w.qw), _ptr(w.scales), _ptr(w.biases),
+                                         _stream(stream)))
+        return w
+
+    def to_blocks36(self, stream=None) -> torch.Tensor:
+        out = torch.empty(self.n * (self.k // 64) * 36, dtype=torch.uint8, device=self.qw.device)
+        _check(lib().kr_q4_to_blocks36(ctypes.byref(self._desc), _ptr(out), _stream(stream)))
+        return out
+
+    def rows(self, lo: int, hi: int) -> "Q4Matrix":
+        return Q4Matrix(self.qw[lo:hi], self.scales[lo:hi], self.biases[lo:hi])
+
+    @property
+    def desc(self):
+        return ctypes.byref(self._desc)
+
+    def nbytes(self) -> int:
+        return self.qw.numel() * 4 + self.scales.numel() * 2 + self.biases.numel() * 2
+
+
+def _out_dtype(dt: int):
+    return torch.float32 if dt == DTYPE_F32 else torch.bfloat16
+
+
+def _dt_of(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    if t.dtype in (torch.bfloat16, torch.int16):
+        return DTYPE_BF16
+    raise ValueError(f"unsupported dtype {t.dtype}")
+
+
+def dequant(w: Q4Matrix, stream=None) -> torch.Tensor:
+    out = torch.empty((w.n, w.k), dtype=torch.float32, device=w.qw.device)
+    _check(lib().kr_q4_dequant(w.desc, _ptr(out), _stream(stream)))
+    return out
+
+
+def f16_to_bf16(t: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    out = torch.empty_like(t) if out is None else out
+    _check(lib().kr_f16_to_bf16(_ptr(t), _ptr(out), t.numel(), _stream(stream)))
+    return out
+
+
+def q4_linear(w: Q4Matrix, x: torch.Tensor, y: Optional[torch.Tensor] = None, out_dtype: int = DTYPE_F32,
+              accumulate: bool = False, stream=None) -> torch.Tensor:
+    """y[m, n] (=|+=) x[m, k] @ W^T.  x is bf16 [m, k] (or [k])."""
+    m = x.numel() // w.k
+    if y is None:
+        y = torch.zeros((m, w.n), dtype=_out_dtype(out_dtype), device=x.device)
+    _check(lib().kr_q4_linear(w.desc, _ptr(x), m, _ptr(y), _dt_of(y), int(accumulate), _stream(stream)))
+    return y
+
+
+def gate_up_act(gate: Q4Matrix, up: Q4Matrix, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                out_dtype: int = DTYPE_F32, activation: int = ACT_SWIGLU, stream=None) -> torch.Tensor:
+    m = x.numel() // gate.k
+    if out is None:
+        out = torch.empty((m, gate.n), dtype=_out_dtype(out_dtype), device=x.device)
+    _check(lib().kr_q4_gate_up_act(gate.desc, up.desc, _ptr(x), m, _ptr(out), _dt_of(out), activation,
+                                   _stream(stream)))
+    return out
+
+
+def mlp_workspace_bytes(m: int, intermediate: int) -> int:
+    return int(lib().kr_q4_mlp_workspace_bytes(m, intermediate))
+
+
+def mlp(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, h: torch.Tensor, x: Optional[torch.Tensor] = None,
+        activation: int = ACT_SWIGLU, workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """h += down(act(gate x) * (up x)) in place; x defaults to h (bf16 h)."""
+    m = h.numel() // down.n
+    need = mlp_workspace_bytes(m, gate.n)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=h.device)
+    _check(lib().kr_q4_mlp(gate.desc, up.desc, down.desc, _ptr(x), _ptr(h), _dt_of(h), m, activation,
+                           _ptr(workspace), workspace.numel(), _stream(stream)))
+    return h
+
+
+# ---- names of the reference operator surface (encoder.rs) -------------------------------
+
+def encode_q4_linear(weight: Q4Matrix, input: torch.Tensor, output: torch.Tensor, m: int, n: int, k: int,
+                     input_byte_offset: int = 0, stream=None) -> None:
+    """encoder.rs:2361-2420: output[m, n] = bf16(input[m, k] @ W^T)."""
+    if (n, k) != (weight.n, weight.k):
+        raise KrError(KR_E_SHAPE, f"weight is [{weight.n},{weight.k}], call says [{n},{k}]")
+    x_ptr = _ptr(input) + input_byte_offset
+    _check(lib().kr_q4_linear(weight.desc, x_ptr, m, _ptr(output), _dt_of(output), 0, _stream(stream)))
+
+
+def encode_q4_linear_accumulate(proj_weight: Q4Matrix, input: torch.Tensor, residual_inout: torch.Tensor,
+                                n: int, k: int, input_byte_offset: int = 0, stream=None) -> None:
+    """encoder.rs:2497-2536: residual[n] = bf16(f32(residual[n]) + W x)."""
+    if (n, k) != (proj_weight.n, proj_weight.k):
+        raise KrError(KR_E_SHAPE, f"weight is [{proj_weight.n},{proj_weight.k}], call says [{n},{k}]")
+    x_ptr = _ptr(input) + input_byte_offset
+    _check(lib().kr_q4_linear(proj_weight.desc, x_ptr, 1, _ptr(residual_inout), _dt_of(residual_inout), 1,
+                              _stream(stream)))
+
+
+def encode_fused_gate_up(gate_weight: Q4Matrix, up_weight: Q4Matrix, input: torch.Tensor,
+                         mlp_hidden: torch.Tensor, m: int, k: int, intermediate_size: int,
+                         activation: int = ACT_SWIGLU, input_byte_offset: int = 0, stream=None) -> None:
+    """encoder.rs:2703-2848: mlp_hidden[m, I] = bf16(act(gate x) * up x)."""
+    if gate_weight.k != k or gate_weight.n != intermediate_size:
+        raise KrError(KR_E_SHAPE, "gate weight shape does not match k / intermediate_size")
+    x_ptr = _ptr(input) + input_byte_offset
+    _check(lib().kr_q4_gate_up_act(gate_weight.desc, up_weight.desc, x_ptr, m, _ptr(mlp_hidden),
+                                   _dt_of(mlp_hidden), activation, _stream(stream)))
+
+
+def encode_dense_mlp(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, norm_out: torch.Tensor,
+                     residual: torch.Tensor, num_tokens: int, hidden_size: int, intermediate_size: int,
+                     activation: int = ACT_SWIGLU, workspace: Optional[torch.Tensor] = None, stream=None) -> None:
+    """encoder.rs:2851-2906: residual += down(act(gate n) * up n) for the normed input n."""
+    if down.n != hidden_size or gate.n != intermediate_size:
+        raise KrError(KR_E_SHAPE, "MLP weights do not match hidden/intermediate sizes")
+    mlp(gate, up, down, residual, x=norm_out, activation=activation, workspace=workspace, stream=stream)

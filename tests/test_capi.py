@@ -1,0 +1,102 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol include/*.h
+declares, and rejects bad arguments before any launch (no GPU work here)."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"\b(kr_\w+)\s*\(", text))
+    return sorted(names)
+
+
+@pytest.fixture(scope="module")
+def kq():
+    import kriya_q4
+
+    if not os.path.exists(kriya_q4.LIB_PATH):
+        kriya_q4.build()
+    kriya_q4.lib()
+    return kriya_q4
+
+
+def test_every_declared_symbol_is_exported(kq):
+    names = declared_functions()
+    assert "kr_q4_linear" in names and "kr_q4_mlp" in names
+    missing = [n for n in names if not hasattr(kq.lib(), n)]
+    assert not missing, missing
+
+
+def test_abi_version_and_options(kq):
+    L = kq.lib()
+    assert L.kr_abi_version() == 1
+    assert L.kr_set_option(kq.OPT_GEMV_ROWS_PER_WAVE, 3) == kq.KR_E_INVALID
+    assert b"rows per wave" in L.kr_last_error()
+    assert L.kr_set_option(999, 1) == kq.KR_E_INVALID
+    old = L.kr_get_option(kq.OPT_GEMV_ROWS_PER_WAVE)
+    assert L.kr_set_option(kq.OPT_GEMV_ROWS_PER_WAVE, 2) == 0
+    assert L.kr_get_option(kq.OPT_GEMV_ROWS_PER_WAVE) == 2
+    assert L.kr_set_option(kq.OPT_GEMV_ROWS_PER_WAVE, old) == 0
+
+
+def _mat(kq, qw=0x10000, sc=0x20000, bi=0x30000, n=8, k=128):
+    return kq.kr_q4_matrix(qw, sc, bi, n, k)
+
+
+def test_linear_argument_checks(kq):
+    L = kq.lib()
+    x, y = 0x40000, 0x50000
+    assert L.kr_q4_linear(None, x, 1, y, kq.DTYPE_F32, 0, None) == kq.KR_E_INVALID
+    assert L.kr_q4_linear(ctypes.byref(_mat(kq, k=96)), x, 1, y, kq.DTYPE_F32, 0, None) == kq.KR_E_SHAPE
+    assert b"multiple of 64" in L.kr_last_error()
+    assert L.kr_q4_linear(ctypes.byref(_mat(kq, k=0)), x, 1, y, kq.DTYPE_F32, 0, None) == kq.KR_E_SHAPE
+    assert L.kr_q4_linear(ctypes.byref(_mat(kq, n=0)), x, 1, y, kq.DTYPE_F32, 0, None) == kq.KR_E_SHAPE
+    assert L.kr_q4_linear(ctypes.byref(_mat(kq, qw=0x10008)), x, 1, y, kq.DTYPE_F32, 0, None) == kq.KR_E_ALIGN
+    assert L.kr_q4_linear(ctypes.byref(_mat(kq, sc=0x20001)), x, 1, y, kq.DTYPE_F32, 0, None) == kq.KR_E_ALIGN
+    assert L.kr_q4_linear(ctypes.byref(_mat(kq, qw=None)), x, 1, y, kq.DTYPE_F32, 0, None) == kq.KR_E_INVALID
+    m = ctypes.byref(_mat(kq))
+    assert L.kr_q4_linear(m, x + 8, 1, y, kq.DTYPE_F32, 0, None) == kq.KR_E_ALIGN
+    assert L.kr_q4_linear(m, x, 1, y + 2, kq.DTYPE_F32, 0, None) == kq.KR_E_ALIGN
+    assert L.kr_q4_linear(m, x, 1, y, 7, 0, None) == kq.KR_E_INVALID
+    assert L.kr_q4_linear(m, x, 1, y, kq.DTYPE_F32, 2, None) == kq.KR_E_INVALID
+    assert L.kr_q4_linear(m, None, 1, y, kq.DTYPE_F32, 0, None) == kq.KR_E_INVALID
+    # empty batch: nothing to do, nothing launched
+    assert L.kr_q4_linear(m, None, 0, None, kq.DTYPE_F32, 0, None) == kq.KR_OK
+
+
+def test_gate_up_and_mlp_argument_checks(kq):
+    L = kq.lib()
+    g, u = _mat(kq, n=192, k=128), _mat(kq, n=192, k=128)
+    bad_u = _mat(kq, n=128, k=128)
+    d = _mat(kq, n=128, k=192)
+    x, out = 0x40000, 0x50000
+    assert L.kr_q4_gate_up_act(ctypes.byref(g), ctypes.byref(bad_u), x, 1, out, 0, 0, None) == kq.KR_E_SHAPE
+    assert L.kr_q4_gate_up_act(ctypes.byref(g), ctypes.byref(u), x, 1, out, 0, 9, None) == kq.KR_E_INVALID
+    need = L.kr_q4_mlp_workspace_bytes(4, 192)
+    assert need >= 4 * 192 * 2 and need % 256 == 0
+    rc = L.kr_q4_mlp(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), x, out, 0, 4, 0, 0x60000, need - 1, None)
+    assert rc == kq.KR_E_WORKSPACE
+    rc = L.kr_q4_mlp(ctypes.byref(g), ctypes.byref(u), ctypes.byref(bad_u), x, out, 0, 4, 0, 0x60000, need, None)
+    assert rc == kq.KR_E_SHAPE
+    rc = L.kr_q4_mlp(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), None, out, kq.DTYPE_F32, 4, 0, 0x60000,
+                     need, None)
+    assert rc == kq.KR_E_INVALID  # an f32 residual needs a separate bf16 input
+
+
+def test_format_argument_checks(kq):
+    L = kq.lib()
+    assert L.kr_q4_from_blocks36(0x1000, 4, 100, 0x2000, 0x3000, 0x4000, None) == kq.KR_E_SHAPE
+    assert L.kr_q4_from_blocks36(0x1002, 4, 128, 0x2000, 0x3000, 0x4000, None) == kq.KR_E_ALIGN
+    assert L.kr_q4_from_blocks36(None, 4, 128, 0x2000, 0x3000, 0x4000, None) == kq.KR_E_INVALID
+    assert L.kr_f16_to_bf16(None, None, 0, None) == kq.KR_OK
+    assert L.kr_f16_to_bf16(0x1001, 0x2000, 4, None) == kq.KR_E_ALIGN
+    assert L.kr_q4_dequant(ctypes.byref(_mat(kq)), 0x1004, None) == kq.KR_E_ALIGN

@@ -1,0 +1,234 @@
+"""GPU parity of the format kernels and the single-token (m == 1) GEMV family
+against the CPU oracle, through the C ABI.
+
+Bars: bit-exact for dequantisation and layout conversion; for matmul outputs
+max |gpu - oracle| <= 1e-2 * RMS(oracle) on f32 outputs, bf16 outputs within
+one bf16 ulp of RNE(oracle).  The reference's own tests use |gpu - cpu| < 0.05
+(test_shader_compile.rs:642-645); that bound is checked too on its fixtures.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from _util import assert_bf16_rounded_close, assert_rms_close, dev_bf16, host_bits, q4_dev, rms
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+FIX = np.load(os.path.join(HERE, "golden", "closed_form.npz"))
+KATS = json.load(open(os.path.join(HERE, "golden", "reference_kats.json")))
+
+
+def synth():
+    from kriya_q4 import synth as s
+    return s
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+# ---------------------------------------------------------------- format kernels
+
+def test_dequant_bit_exact_config0(kq):
+    s = synth()
+    case("dequant cfg0 11008x2048 seed 0")
+    wq = s.q4_weight(11008, 2048, 0)
+    got = kq.dequant(q4_dev(kq, wq)).cpu().numpy()
+    want = O.dequant_planar(O.Q4Planar(*wq))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_bit_exact_extreme_scales(kq):
+    case("dequant extreme bf16 scale/bias bit patterns")
+    rng = np.random.default_rng(5)
+    n, k = 64, 512
+    qw = rng.integers(0, 1 << 32, size=(n, k // 8), dtype=np.uint64).astype(np.uint32)
+    sc = rng.integers(0, 1 << 16, size=(n, k // 64), dtype=np.uint64).astype(np.uint16)
+    bi = rng.integers(0, 1 << 16, size=(n, k // 64), dtype=np.uint64).astype(np.uint16)
+    sc[0, :4] = [0x7F80, 0xFF80, 0x0001, 0x8000]  # inf, -inf, subnormal, -0
+    bi[0, :4] = [0xFF80, 0x7F80, 0x8000, 0x0001]
+    got = kq.dequant(q4_dev(kq, (qw, sc, bi))).cpu().numpy()
+    want = O.dequant_planar(O.Q4Planar(qw, sc, bi))
+    both_nan = np.isnan(got) & np.isnan(want)
+    assert np.array_equal(np.where(both_nan, 0, got.view(np.uint32)), np.where(both_nan, 0, want.view(np.uint32)))
+
+
+def test_blocks36_round_trip_on_gpu(kq):
+    case("blocks36 -> planar -> blocks36, 1000 LCG blocks + patterns")
+    lcg = np.array(KATS["lcg_blocks_1000"], np.uint8)  # 8 rows x 125 groups
+    dev = torch.from_numpy(lcg.ravel().copy()).cuda()
+    w = kq.Q4Matrix.from_blocks36(dev, 8, 125 * 64)
+    ref = O.blocks36_to_planar(lcg, 8, 125 * 64)
+    assert np.array_equal(w.qw.cpu().numpy().view(np.uint32), ref.qw)
+    assert np.array_equal(w.scales.cpu().numpy().view(np.uint16), ref.scales)
+    assert np.array_equal(w.biases.cpu().numpy().view(np.uint16), ref.biases)
+    back = w.to_blocks36().cpu().numpy().reshape(-1, 36)
+    assert np.array_equal(back, lcg)
+
+
+def test_blocks36_config0_planar_equivalence(kq):
+    case("cfg0 planar -> blocks36 (oracle) -> planar (gpu)")
+    wq = synth().q4_weight(11008, 2048, 0)
+    blocks = O.planar_to_blocks36(O.Q4Planar(*wq))
+    w = kq.Q4Matrix.from_blocks36(torch.from_numpy(blocks.ravel()).cuda(), 11008, 2048)
+    assert np.array_equal(w.qw.cpu().numpy().view(np.uint32), wq[0])
+    assert np.array_equal(w.scales.cpu().numpy().view(np.uint16), wq[1])
+
+
+def test_f16_to_bf16_all_patterns(kq):
+    case("f16 -> bf16, all 65536 patterns")
+    h = np.arange(1 << 16, dtype=np.uint16)
+    got = host_bits(kq.f16_to_bf16(torch.from_numpy(h.view(np.int16)).cuda()))
+    want = np.array([O.half_to_bf16(int(v), True) for v in h], np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------- GEMV m == 1
+
+@pytest.mark.parametrize("name", ["gemv_5x64", "gemv_7x128", "gemv_19x128", "persist_256"])
+def test_gemv_reference_fixtures(kq, name):
+    case(f"gemv fixture {name}")
+    w = q4_dev(kq, (FIX[f"{name}_qw"], FIX[f"{name}_sc"], FIX[f"{name}_bi"]))
+    x = dev_bf16(FIX[f"{name}_x"])
+    want = FIX[f"{name}_y"]
+    y32 = kq.q4_linear(w, x, out_dtype=kq.DTYPE_F32).cpu().numpy()[0]
+    assert np.max(np.abs(y32 - want)) < 0.05  # the reference test's own bound
+    assert_rms_close(y32, want, what=name)
+    yb = kq.q4_linear(w, x, out_dtype=kq.DTYPE_BF16)
+    assert_bf16_rounded_close(host_bits(yb)[0], want, rms(want), what=name)
+
+
+def test_gemv_config0_full_size(kq):
+    s = synth()
+    case("gemv cfg0 11008x2048 seed 0, f32 and bf16 outputs")
+    wq = s.q4_weight(11008, 2048, 0)
+    x = s.bf16_normal((1, 2048), 1)
+    w = q4_dev(kq, wq)
+    y = kq.q4_linear(w, dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy()[0]
+    want = O.q4_matmul(O.Q4Planar(*wq), x)[0]
+    gold = O.q4_matmul_f64(O.Q4Planar(*wq), x)[0]
+    err = assert_rms_close(y, want, what="cfg0")
+    print(f"cfg0: max|gpu-oracle| = {err:.3e} ({err / rms(want):.2e} of rms), "
+          f"max|gpu-f64| = {np.max(np.abs(y - gold)):.3e}, max|oracle-f64| = {np.max(np.abs(want - gold)):.3e}")
+    yb = kq.q4_linear(w, dev_bf16(x), out_dtype=kq.DTYPE_BF16)
+    assert_bf16_rounded_close(host_bits(yb)[0], want, rms(want), what="cfg0 bf16")
+
+
+@pytest.mark.parametrize("n,k", [(1, 64), (3, 128), (19, 512), (37, 1024), (73, 512), (129, 1408),
+                                 (64, 11008), (2048, 11008), (300, 2048 + 64)])
+def test_gemv_shapes(kq, n, k):
+    s = synth()
+    case(f"gemv n={n} k={k}")
+    wq = s.q4_weight(n, k, 100 + n + k)
+    x = s.bf16_normal((1, k), 200 + n)
+    want = O.q4_matmul(O.Q4Planar(*wq), x)[0]
+    for rpw in (1, 2, 4, 8):
+        kq.set_option(kq.OPT_GEMV_ROWS_PER_WAVE, rpw)
+        try:
+            y = kq.q4_linear(q4_dev(kq, wq), dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy()[0]
+        finally:
+            kq.set_option(kq.OPT_GEMV_ROWS_PER_WAVE, 4)
+        assert_rms_close(y, want, what=f"n={n} k={k} rows/wave={rpw}")
+
+
+def test_gemv_accumulate_modes(kq):
+    s = synth()
+    case("gemv accumulate f32 and bf16 (cfg1 down shape 2048x11008)")
+    wq = s.q4_weight(2048, 11008, 1003)
+    x = s.bf16_normal((1, 11008), 7)
+    r0 = s.bf16_normal((1, 2048), 8)
+    w = q4_dev(kq, wq)
+    y = O.q4_matmul(O.Q4Planar(*wq), x)[0]
+    # f32 residual: res += y
+    res32 = torch.from_numpy(O.bf16_to_f32(r0)).cuda()
+    kq.q4_linear(w, dev_bf16(x), y=res32, accumulate=True)
+    assert_rms_close(res32.cpu().numpy()[0] - O.bf16_to_f32(r0)[0], y, what="acc f32")
+    # bf16 residual in place: res = bf16(f32(res) + y)
+    res16 = dev_bf16(r0).clone()
+    kq.encode_q4_linear_accumulate(w, dev_bf16(x), res16, 2048, 11008)
+    want = O.bf16_to_f32(r0)[0] + y
+    assert_bf16_rounded_close(host_bits(res16)[0], want, rms(y), what="acc bf16")
+
+
+def test_gemv_grid_invariance_and_determinism(kq):
+    case("gemv persistent grid (4 blocks) vs full grid, bitwise; 3 repeated runs")
+    w = q4_dev(kq, (FIX["persist_256_qw"], FIX["persist_256_sc"], FIX["persist_256_bi"]))
+    x = dev_bf16(FIX["persist_256_x"])
+    full = host_bits(kq.q4_linear(w, x, out_dtype=kq.DTYPE_BF16))
+    kq.set_option(kq.OPT_GEMV_MAX_BLOCKS, 4)
+    try:
+        small = host_bits(kq.q4_linear(w, x, out_dtype=kq.DTYPE_BF16))
+    finally:
+        kq.set_option(kq.OPT_GEMV_MAX_BLOCKS, 0)
+    assert np.array_equal(full, small)
+    s = synth()
+    wq = s.q4_weight(11008, 2048, 0)
+    xb = dev_bf16(s.bf16_normal((1, 2048), 1))
+    wd = q4_dev(kq, wq)
+    runs = [kq.q4_linear(wd, xb, out_dtype=kq.DTYPE_F32).cpu().numpy() for _ in range(3)]
+    assert all(np.array_equal(runs[0].view(np.uint32), r.view(np.uint32)) for r in runs[1:])
+
+
+def test_gemv_multi_token_rows(kq):
+    s = synth()
+    case("linear m=3, k=2048, n=1000")
+    wq = s.q4_weight(1000, 2048, 31)
+    x = s.bf16_normal((3, 2048), 32)
+    y = kq.q4_linear(q4_dev(kq, wq), dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy()
+    assert_rms_close(y, O.q4_matmul(O.Q4Planar(*wq), x), what="m=3")
+
+
+# ---------------------------------------------------------------- gate+up+act and MLP
+
+@pytest.mark.parametrize("name", ["swiglu_9x128", "swiglu_11x128"])
+def test_gate_up_reference_fixtures(kq, name):
+    case(f"gate_up fixture {name}")
+    g = q4_dev(kq, (FIX[f"{name}_gqw"], FIX[f"{name}_gsc"], FIX[f"{name}_gbi"]))
+    u = q4_dev(kq, (FIX[f"{name}_uqw"], FIX[f"{name}_usc"], FIX[f"{name}_ubi"]))
+    x = dev_bf16(FIX[f"{name}_x"])
+    want = FIX[f"{name}_a"]
+    a = kq.gate_up_act(g, u, x, out_dtype=kq.DTYPE_F32).cpu().numpy()[0]
+    assert np.max(np.abs(a - want)) < 0.05
+    assert_rms_close(a, want, what=name)
+    ab = kq.gate_up_act(g, u, x, out_dtype=kq.DTYPE_BF16)
+    assert_bf16_rounded_close(host_bits(ab)[0], want, rms(want), what=name)
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_gate_up_config1_shapes(kq, act):
+    s = synth()
+    case(f"gate_up cfg1 11008x2048 act={act}")
+    g, u = s.q4_weight(11008, 2048, 1001), s.q4_weight(11008, 2048, 1002)
+    x = s.bf16_normal((1, 2048), 1004)
+    a = kq.gate_up_act(q4_dev(kq, g), q4_dev(kq, u), dev_bf16(x), out_dtype=kq.DTYPE_F32,
+                       activation=act).cpu().numpy()
+    want = O.q4_gate_up_act(O.Q4Planar(*g), O.Q4Planar(*u), x, variant=act)
+    assert_rms_close(a, want, what=f"gate_up act={act}")
+
+
+@pytest.mark.parametrize("B", [1, 4, 16])
+def test_mlp_config1(kq, B):
+    s = synth()
+    case(f"mlp cfg1 B={B}: h += down(silu(gate h) * up h), h bf16 in place")
+    g, u = s.q4_weight(11008, 2048, 1001), s.q4_weight(11008, 2048, 1002)
+    d = s.q4_weight(2048, 11008, 1003)
+    h0 = s.bf16_normal((B, 2048), 1010 + B)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    delta = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), h0)
+    h = dev_bf16(h0).clone()
+    kq.mlp(G, U, D, h)
+    want = O.bf16_to_f32(h0) + delta
+    assert_bf16_rounded_close(host_bits(h), want, rms(delta), what=f"mlp B={B} bf16 residual")
+    # f32 residual stream: exposes the MLP output itself to the RMS bar
+    h32 = torch.from_numpy(O.bf16_to_f32(h0)).cuda()
+    kq.mlp(G, U, D, h32, x=dev_bf16(h0))
+    got = h32.cpu().numpy() - O.bf16_to_f32(h0)
+    err = assert_rms_close(got, delta, what=f"mlp B={B}")
+    delta32 = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), h0, bf16_intermediate=False)
+    print(f"mlp B={B}: max err vs oracle {err / rms(delta):.2e} of rms; vs f32-intermediate oracle "
+          f"{np.max(np.abs(got - delta32)) / rms(delta32):.2e} of rms")
+    assert_rms_close(got, delta32, what=f"mlp B={B} vs f32 intermediate")
