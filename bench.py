@@ -88,7 +88,7 @@ def bench_mlp(kq, torch, synth, B, copies, steps, warmup):
     planars = [synth.q4_weight(I, H, 1001), synth.q4_weight(I, H, 1002), synth.q4_weight(H, I, 1003)]
     rot = Rotation(kq, torch, planars, copies)
     h = torch.from_numpy(synth.bf16_normal((B, H), 1010 + B).view(np.int16)).cuda().view(torch.bfloat16)
-    ws = torch.empty(kq.mlp_workspace_bytes(B, I), dtype=torch.uint8, device="cuda")
+    ws = kq.mlp_workspace(B, I)
     xs = h.clone()  # MLP input (bf16); h is the residual stream updated in place
 
     def step(i):
@@ -207,8 +207,9 @@ def main():
         "data": f"synthetic: seeded SplitMix64 weights (config-0 distribution), {args.copies} rotating weight "
                 f"copies ({args.copies * 3 * Q4_BYTES(11008, 2048) / 1e9:.2f} GB) so HBM, not MALL, serves them",
         "config": {"workload": "cfg1_fused_mlp_decode_B1", "hidden": 2048, "intermediate": 11008, "batch": 1,
-                   "weights": "Q4_G64 gate/up [11008,2048], down [2048,11008]", "graph": "HIP graph replay"},
-        "roofline": {"bound": "hbm", "kernel": "q4_gemv_dot2 gate_up_act (gate+up+silu, m=1)",
+                   "weights": "Q4_G64 gate/up [11008,2048], down [2048,11008]",
+                   "launches_per_step": 2, "graph": "HIP graph replay"},
+        "roofline": {"bound": "hbm", "kernel": "q4_gemv_wave_kernel<R,1,kGateUpBF16> (gate+up+silu fused, m=1)",
                      "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
                      "alg_bytes_per_launch": dom["alg_bytes"], "avg_launch_us": round(dom["s"] * 1e6, 3)},

@@ -74,8 +74,13 @@ const char *kr_last_error(void);
 /* Process-wide launch tuning (no counterpart in the reference, whose launch
  * shapes are fixed in encoder.rs).  Not synchronised with calls in flight on
  * other threads.  Results never depend on these values. */
-#define KR_OPT_GEMV_ROWS_PER_WAVE 1 /* 1, 2, 4 (default) or 8                  */
-#define KR_OPT_GEMV_MAX_BLOCKS 2    /* 0 (default): one pass; > 0: grid-stride */
+#define KR_OPT_GEMV_ROWS_PER_WAVE 1     /* rows per wave tile: 1, 2 (default), 4 or 8     */
+#define KR_OPT_GEMV_MAX_BLOCKS 2        /* 0 (default): no cap; > 0: cap on the grid       */
+#define KR_OPT_GEMV_SPLIT_K_CHUNKS 3    /* m == 1 rows of >= value 16-byte chunks use the
+                                           split-K block kernel (always for k > 4096);
+                                           0 (default): only beyond k = 4096               */
+#define KR_OPT_GEMV_BLOCK_ROWS 4        /* rows per split-K block tile: 1, 2 (default), 4, 8 */
+#define KR_OPT_GEMV_PERSISTENT_BLOCKS 5 /* grid of the persistent wave kernel (1024)       */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 
@@ -129,7 +134,8 @@ int kr_q4_gate_up_act(const kr_q4_matrix *gate, const kr_q4_matrix *up,
  * of h; for h_dtype f32 a separate bf16 input x must be given (x may be NULL
  * when h_dtype is bf16, then x = h).  The intermediate activation is kept in
  * bf16 in the workspace, as the reference stores it.
- * workspace: device memory of at least kr_q4_mlp_workspace_bytes(m, gate->n). */
+ * workspace: device memory of at least kr_q4_mlp_workspace_bytes(m, gate->n),
+ * 16-byte aligned; calls that share a workspace must not overlap in time. */
 size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t intermediate);
 int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down,
               const uint16_t *x, void *h, int h_dtype, uint32_t m, int activation,

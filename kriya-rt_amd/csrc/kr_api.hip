@@ -53,6 +53,7 @@ int check_matrix(const kr_q4_matrix *w, const char *name) {
     if (!aligned(w->scales, 2) || !aligned(w->biases, 2))
         return fail(KR_E_ALIGN, "%s: scales/biases must be 2-byte aligned", name);
     if ((uint64_t)w->n * (w->k / 8) > (1ull << 40)) return fail(KR_E_SHAPE, "%s: matrix too large", name);
+    if (w->k > kMaxGemvK) return fail(KR_E_SHAPE, "%s: k=%u exceeds the supported maximum %u", name, w->k, kMaxGemvK);
     return KR_OK;
 }
 
@@ -87,6 +88,19 @@ int kr_set_option(int option, int value) {
             if (value < 0) return fail(KR_E_INVALID, "max blocks must be >= 0");
             tuning().gemv_max_blocks = value;
             return ok();
+        case KR_OPT_GEMV_SPLIT_K_CHUNKS:
+            if (value < 0) return fail(KR_E_INVALID, "split-k threshold must be >= 0");
+            tuning().gemv_split_k_chunks = value;
+            return ok();
+        case KR_OPT_GEMV_BLOCK_ROWS:
+            if (value != 1 && value != 2 && value != 4 && value != 8)
+                return fail(KR_E_INVALID, "block rows must be 1, 2, 4 or 8");
+            tuning().gemv_block_rows = value;
+            return ok();
+        case KR_OPT_GEMV_PERSISTENT_BLOCKS:
+            if (value < 1) return fail(KR_E_INVALID, "persistent blocks must be >= 1");
+            tuning().gemv_persistent_blocks = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -95,6 +109,9 @@ int kr_get_option(int option) {
     switch (option) {
         case KR_OPT_GEMV_ROWS_PER_WAVE: return tuning().gemv_rows_per_wave;
         case KR_OPT_GEMV_MAX_BLOCKS: return tuning().gemv_max_blocks;
+        case KR_OPT_GEMV_SPLIT_K_CHUNKS: return tuning().gemv_split_k_chunks;
+        case KR_OPT_GEMV_BLOCK_ROWS: return tuning().gemv_block_rows;
+        case KR_OPT_GEMV_PERSISTENT_BLOCKS: return tuning().gemv_persistent_blocks;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }

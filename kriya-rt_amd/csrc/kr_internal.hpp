@@ -23,10 +23,17 @@ enum GemvEpilogue : int {
 // Runtime tuning knobs (set through kr_set_option for sweeps; defaults are the
 // measured best on MI355X).
 struct Tuning {
-    int gemv_rows_per_wave = 4;   // 1, 2, 4 or 8
-    int gemv_max_blocks = 0;      // 0 = one pass, no grid-stride loop
+    int gemv_rows_per_wave = 2;        // rows per wave tile: 1, 2, 4 or 8
+    int gemv_block_rows = 2;           // rows per split-K block tile: 1, 2, 4 or 8
+    int gemv_max_blocks = 0;           // > 0: cap on the grid (tests use it for grid invariance)
+    int gemv_persistent_blocks = 1024; // grid of the persistent wave kernel
+    int gemv_split_k_chunks = 0;       // rows of >= this many 16-byte chunks use the block kernel
+                                       // (always beyond 128 chunks); 0 = default
 };
 Tuning &tuning();
+
+// Largest k of the m == 1 kernels (three 16-byte chunks per thread of a 256-thread block).
+constexpr uint32_t kMaxGemvK = 3 * 256 * 32;
 
 hipError_t launch_format_dequant(const Q4Mat &w, float *out, hipStream_t s);
 hipError_t launch_from_blocks36(const void *blocks, uint32_t n, uint32_t k, uint32_t *qw, uint16_t *sc,

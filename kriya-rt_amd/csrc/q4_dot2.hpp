@@ -1,0 +1,128 @@
+// q4_dot2.hpp — the shared inner step of the m == 1 Q4_G64 kernels (GEMV
+// family and fused MLP): nibble unpack by bit patterns + v_dot2_f32_bf16.
+//
+// Arithmetic per 8 nibbles (one u32 word): 3 shifts + 4 v_and_or_b32 turn the
+// nibble pairs (j, j+4) into exact bf16 values (128+q) (kr_device.hpp), and
+// 4 v_dot2_f32_bf16 multiply them with the matching x pairs.  A chunk is 16
+// bytes = 32 elements = half a 64-group; per row and chunk the affine map
+// costs two FMAs:  acc += s * D + (b - 128 s) * sum(x).
+#pragma once
+
+#include "kr_internal.hpp"
+
+namespace kr {
+
+// Constants placed in registers through an opaque move, so that the compiler
+// cannot fold them into literals: gfx9 VOP3 encodings (v_and_or_b32,
+// v_perm_b32) take no literal operand, and with literals the unpack splits
+// into separate AND and OR instructions.
+__device__ __forceinline__ uint32_t sgpr_const(uint32_t v) {
+    uint32_t r;
+    asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
+    return r;
+}
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
+    uint32_t r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
+    return r;
+}
+
+// x operand of one chunk: the 16 dot2 pairs P[4w + j] = (x_{8w+j}, x_{8w+j+4})
+// and the chunk sum.
+struct XChunk {
+    uint32_t p[16];
+    float sum;
+};
+
+__device__ __forceinline__ void load_xchunk(XChunk &xc, const uint16_t *__restrict__ x, uint32_t c, uint32_t sel_lo,
+                                            uint32_t sel_hi) {
+    const u32x4 *xv = reinterpret_cast<const u32x4 *>(x) + 4 * c;
+    const u32x4 v0 = xv[0], v1 = xv[1], v2 = xv[2], v3 = xv[3];
+    const uint32_t X[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
+                            v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        xc.p[4 * w + 0] = __builtin_amdgcn_perm(X[4 * w + 2], X[4 * w + 0], sel_lo);
+        xc.p[4 * w + 1] = __builtin_amdgcn_perm(X[4 * w + 2], X[4 * w + 0], sel_hi);
+        xc.p[4 * w + 2] = __builtin_amdgcn_perm(X[4 * w + 3], X[4 * w + 1], sel_lo);
+        xc.p[4 * w + 3] = __builtin_amdgcn_perm(X[4 * w + 3], X[4 * w + 1], sel_hi);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s = dot2_bf16(X[i], 0x3F803F80u, s);
+    xc.sum = s;
+}
+
+// acc += s * sum_j (128 + q_j) x_j + (b - 128 s) * sum(x) over one chunk of one row.
+__device__ __forceinline__ float chunk_dot(const u32x4 &wv, uint32_t sraw, uint32_t braw, const XChunk &xc, float acc,
+                                           uint32_t mask, uint32_t magic) {
+    const float s = bf16_to_f32(sraw);
+    const float b = bf16_to_f32(braw);
+    const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+    float d = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) d = dot2_bf16(((wd[w] >> (4 * j)) & mask) | magic, xc.p[4 * w + j], d);
+    }
+    return fmaf(s, d, fmaf(fmaf(-128.0f, s, b), xc.sum, acc));
+}
+
+template <int EPI>
+__device__ __forceinline__ void store_row(void *out, uint32_t row, float v) {
+    if (EPI == kStoreF32) {
+        reinterpret_cast<float *>(out)[row] = v;
+    } else if (EPI == kStoreBF16) {
+        reinterpret_cast<uint16_t *>(out)[row] = (uint16_t)f32_to_bf16(v);
+    } else if (EPI == kAccF32) {
+        reinterpret_cast<float *>(out)[row] += v;
+    } else if (EPI == kAccBF16) {  // res = bf16(f32(res) + y), q4_gemm_and_moe.metal:1407-1420
+        uint16_t *o = reinterpret_cast<uint16_t *>(out);
+        o[row] = (uint16_t)f32_to_bf16(v + bf16_to_f32(o[row]));
+    } else if (EPI == kGateUpF32) {
+        reinterpret_cast<float *>(out)[row] = v;
+    } else {
+        reinterpret_cast<uint16_t *>(out)[row] = (uint16_t)f32_to_bf16(v);
+    }
+}
+
+// Row r of tile t: plain rows t*R + r, or (gate, up) rows of channel t*R/2 + r/2.
+template <int R, bool kGateUp>
+__device__ __forceinline__ void tile_rows(const Q4Mat &A, const Q4Mat &B, uint32_t t, const u32x4 *(&rq)[R],
+                                          const uint16_t *(&rs)[R], const uint16_t *(&rb)[R]) {
+    const uint32_t wpr = A.k >> 3, groups = A.k >> 6;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        uint32_t row;
+        const Q4Mat *m = &A;
+        if (kGateUp) {
+            row = t * (R / 2) + (r >> 1);
+            if (r & 1) m = &B;
+        } else {
+            row = t * R + r;
+        }
+        row = row < A.n ? row : A.n - 1;  // tail rows re-read a valid row and are never stored
+        rq[r] = reinterpret_cast<const u32x4 *>(m->qw + (size_t)row * wpr);
+        rs[r] = m->sc + (size_t)row * groups;
+        rb[r] = m->bi + (size_t)row * groups;
+    }
+}
+
+template <int R, int EPI>
+__device__ __forceinline__ void tile_epilogue(float tot, int lane, uint32_t t, uint32_t nrows, void *out, int act) {
+    constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
+    constexpr int kSeg = kWave / R;
+    const int slot = lane / kSeg;
+    if (kGateUp) {
+        const float up = __shfl_xor(tot, kSeg);
+        if ((lane % kSeg) == 0 && (slot & 1) == 0) {
+            const uint32_t ch = t * (R / 2) + (slot >> 1);
+            if (ch < nrows) store_row<EPI>(out, ch, activation(tot, act) * up);
+        }
+    } else if ((lane % kSeg) == 0) {
+        const uint32_t row = t * R + slot;
+        if (row < nrows) store_row<EPI>(out, row, tot);
+    }
+}
+
+}  // namespace kr

@@ -27,7 +27,8 @@ KR_OK = 0
 KR_E_INVALID, KR_E_SHAPE, KR_E_ALIGN, KR_E_HIP, KR_E_WORKSPACE, KR_E_UNSUPPORTED = -1, -2, -3, -4, -5, -6
 DTYPE_BF16, DTYPE_F32 = 0, 1
 ACT_SWIGLU, ACT_GEGLU, ACT_RELU = 0, 1, 2
-OPT_GEMV_ROWS_PER_WAVE, OPT_GEMV_MAX_BLOCKS = 1, 2
+OPT_GEMV_ROWS_PER_WAVE, OPT_GEMV_MAX_BLOCKS, OPT_GEMV_SPLIT_K_CHUNKS = 1, 2, 3
+OPT_GEMV_BLOCK_ROWS, OPT_GEMV_PERSISTENT_BLOCKS = 4, 5
 
 _lib = None
 
@@ -201,13 +202,17 @@ def mlp_workspace_bytes(m: int, intermediate: int) -> int:
     return int(lib().kr_q4_mlp_workspace_bytes(m, intermediate))
 
 
+def mlp_workspace(m: int, intermediate: int, device="cuda") -> torch.Tensor:
+    """Device workspace of an MLP call (the bf16 intermediate)."""
+    return torch.empty(mlp_workspace_bytes(m, intermediate), dtype=torch.uint8, device=device)
+
+
 def mlp(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, h: torch.Tensor, x: Optional[torch.Tensor] = None,
         activation: int = ACT_SWIGLU, workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
     """h += down(act(gate x) * (up x)) in place; x defaults to h (bf16 h)."""
     m = h.numel() // down.n
-    need = mlp_workspace_bytes(m, gate.n)
     if workspace is None:
-        workspace = torch.empty(need, dtype=torch.uint8, device=h.device)
+        workspace = mlp_workspace(m, gate.n, device=h.device)
     _check(lib().kr_q4_mlp(gate.desc, up.desc, down.desc, _ptr(x), _ptr(h), _dt_of(h), m, activation,
                            _ptr(workspace), workspace.numel(), _stream(stream)))
     return h

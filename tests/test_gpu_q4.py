@@ -131,7 +131,7 @@ def test_gemv_shapes(kq, n, k):
         try:
             y = kq.q4_linear(q4_dev(kq, wq), dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy()[0]
         finally:
-            kq.set_option(kq.OPT_GEMV_ROWS_PER_WAVE, 4)
+            kq.set_option(kq.OPT_GEMV_ROWS_PER_WAVE, 2)
         assert_rms_close(y, want, what=f"n={n} k={k} rows/wave={rpw}")
 
 
@@ -232,3 +232,71 @@ def test_mlp_config1(kq, B):
     print(f"mlp B={B}: max err vs oracle {err / rms(delta):.2e} of rms; vs f32-intermediate oracle "
           f"{np.max(np.abs(got - delta32)) / rms(delta32):.2e} of rms")
     assert_rms_close(got, delta32, what=f"mlp B={B} vs f32 intermediate")
+
+
+# ---------------------------------------------------------------- MLP (m == 1): shapes, reuse, graphs
+
+@pytest.mark.parametrize("hidden,inter", [(2048, 11008), (256, 384), (512, 1408), (1024, 4096)])
+def test_mlp_m1_shapes_and_workspace_reuse(kq, hidden, inter):
+    s = synth()
+    case(f"mlp m=1 hidden={hidden} inter={inter}: 3 calls on one workspace, f32 residual")
+    g, u = s.q4_weight(inter, hidden, 21), s.q4_weight(inter, hidden, 22)
+    d = s.q4_weight(hidden, inter, 23)
+    h0 = s.bf16_normal((1, hidden), 24)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    delta = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), h0)
+    ws = kq.mlp_workspace(1, inter)
+    h32 = torch.from_numpy(O.bf16_to_f32(h0)).cuda()
+    x = dev_bf16(h0)
+    outs = []
+    for _ in range(3):
+        kq.mlp(G, U, D, h32, x=x, workspace=ws)
+        outs.append(h32.cpu().numpy().copy())
+    base = O.bf16_to_f32(h0)
+    assert_rms_close(outs[0] - base, delta, what="call 1")
+    assert_rms_close(outs[2] - outs[1], delta, rel=2e-2, what="call 3")  # f32 residual rounding grows
+
+
+def test_mlp_bf16_in_place_and_determinism(kq):
+    s = synth()
+    case("mlp m=1 cfg1, bf16 h in place (x = h), 2 runs bitwise equal")
+    g, u = s.q4_weight(11008, 2048, 1001), s.q4_weight(11008, 2048, 1002)
+    d = s.q4_weight(2048, 11008, 1003)
+    h0 = s.bf16_normal((1, 2048), 1011)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    delta = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), h0)
+    runs = []
+    for _ in range(2):
+        h = dev_bf16(h0).clone()
+        kq.mlp(G, U, D, h)
+        runs.append(host_bits(h))
+    assert np.array_equal(runs[0], runs[1])
+    assert_bf16_rounded_close(runs[0], O.bf16_to_f32(h0) + delta, rms(delta), what="bf16 in place")
+
+
+def test_mlp_graph_replays(kq):
+    s = synth()
+    case("mlp m=1 captured in a HIP graph, 3 replays vs eager")
+    g, u = s.q4_weight(11008, 2048, 1001), s.q4_weight(11008, 2048, 1002)
+    d = s.q4_weight(2048, 11008, 1003)
+    h0 = s.bf16_normal((1, 2048), 1011)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    ws = kq.mlp_workspace(1, 11008)
+    x = dev_bf16(h0)
+    h = torch.zeros((1, 2048), dtype=torch.float32, device="cuda")
+    kq.mlp(G, U, D, h, x=x, workspace=ws)
+    eager = h.cpu().numpy().copy()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        h.zero_()
+        with torch.cuda.graph(graph, stream=stream):
+            kq.mlp(G, U, D, h, x=x, workspace=ws)
+    torch.cuda.synchronize()
+    for i in range(3):
+        h.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(h.cpu().numpy().view(np.uint32), eager.view(np.uint32)), f"replay {i}"
