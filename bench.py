@@ -88,7 +88,7 @@ def bench_mlp(kq, torch, synth, B, copies, steps, warmup):
     planars = [synth.q4_weight(I, H, 1001), synth.q4_weight(I, H, 1002), synth.q4_weight(H, I, 1003)]
     rot = Rotation(kq, torch, planars, copies)
     h = torch.from_numpy(synth.bf16_normal((B, H), 1010 + B).view(np.int16)).cuda().view(torch.bfloat16)
-    ws = kq.mlp_workspace(B, I)
+    ws = kq.mlp_workspace(B, H, I)
     xs = h.clone()  # MLP input (bf16); h is the residual stream updated in place
 
     def step(i):

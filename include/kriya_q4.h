@@ -127,6 +127,18 @@ int kr_q4_gate_up_act(const kr_q4_matrix *gate, const kr_q4_matrix *up,
                       const uint16_t *x, uint32_t m, void *act_out, int act_dtype,
                       int activation, void *stream);
 
+/* ---- fused Q/K/V projections: encoder.rs:2539-2619 (encode_fused_qkv;
+ *      kernels q4_g64_decode_qkv_gemv* and q4_g64_batched_simdgroup_qkv_gemm_m64,
+ *      q4_gemm_and_moe.metal:1564-1793, 2853-3022) ----
+ * q_out[i] = x_i . q^T (+ q_bias), same for k and v; q, k, v share k (hidden).
+ * Biases are bf16 [n] or NULL (Qwen2 has them, quantizer.rs:395).  Outputs are
+ * [m, n] of out_dtype; for bf16 the stored value is RNE(f32 dot + f32 bias).
+ * m > 1 runs the three projections in one launch. */
+int kr_q4_qkv(const kr_q4_matrix *q, const kr_q4_matrix *k, const kr_q4_matrix *v,
+              const uint16_t *q_bias, const uint16_t *k_bias, const uint16_t *v_bias,
+              const uint16_t *x, uint32_t m, void *q_out, void *k_out, void *v_out,
+              int out_dtype, void *stream);
+
 /* ---- dense MLP: encoder.rs:2851-2906 (encode_dense_mlp) ----
  * h[i, :] += down . bf16(act(gate . h_i) * (up . h_i))   for i < m
  * The residual h is read as bf16 and updated in place (h_dtype bf16: stored
@@ -134,9 +146,11 @@ int kr_q4_gate_up_act(const kr_q4_matrix *gate, const kr_q4_matrix *up,
  * of h; for h_dtype f32 a separate bf16 input x must be given (x may be NULL
  * when h_dtype is bf16, then x = h).  The intermediate activation is kept in
  * bf16 in the workspace, as the reference stores it.
- * workspace: device memory of at least kr_q4_mlp_workspace_bytes(m, gate->n),
- * 16-byte aligned; calls that share a workspace must not overlap in time. */
-size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t intermediate);
+ * workspace: device memory of at least
+ * kr_q4_mlp_workspace_bytes(m, gate->k, gate->n), 16-byte aligned; calls that
+ * share a workspace must not overlap in time.  For m > 1 the workspace also
+ * holds split-K partial sums of the down projection, reduced in a fixed order. */
+size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermediate);
 int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down,
               const uint16_t *x, void *h, int h_dtype, uint32_t m, int activation,
               void *workspace, size_t workspace_bytes, void *stream);

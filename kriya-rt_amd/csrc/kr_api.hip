@@ -6,6 +6,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <string>
 
 #include "kriya_q4.h"
@@ -65,6 +66,113 @@ bool valid_dtype(int dt) { return dt == KR_DTYPE_BF16 || dt == KR_DTYPE_F32; }
 bool valid_act(int a) { return a == KR_ACT_SWIGLU || a == KR_ACT_GEGLU || a == KR_ACT_RELU; }
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+constexpr uint32_t kMaxSplitK = 8;
+
+int device_cus() {
+    static thread_local int dev = -1, cus = 0;
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess) d = 0;
+    if (d != dev) {
+        dev = d;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || cus <= 0) cus = 256;
+    }
+    return cus;
+}
+
+// M tile class of the matrix-core kernels: 32-row tiles for batched decode,
+// 64 or 128 rows for prefill.
+int bm_class(uint32_t m) { return m <= 16 ? 16 : (m <= 64 ? 64 : 128); }
+int bn_of(int bm, bool gate_up) { return bm <= 16 ? 32 : (gate_up ? 64 : 64); }
+int bm_rows(int bm) { return bm <= 16 ? 32 : bm; }
+
+MfmaArgs mfma_args(const uint16_t *x, uint32_t m, uint32_t k, int out_dtype, int accumulate) {
+    MfmaArgs a{};
+    a.x = x;
+    a.m = m;
+    a.k = k;
+    a.ldx = k;
+    a.out_f32 = out_dtype == KR_DTYPE_F32;
+    a.accumulate = accumulate;
+    a.ksplit = 1;
+    a.groups_per_split = k / 64;
+    return a;
+}
+
+MfmaProblem problem(const Q4Mat &w, const Q4Mat *w2, void *out, const uint16_t *bias, uint32_t ldo) {
+    MfmaProblem p{};
+    p.w = w;
+    if (w2) p.w2 = *w2;
+    p.out = out;
+    p.bias = bias;
+    p.ldo = ldo;
+    return p;
+}
+
+// Few-token matmul on the skinny kernel.  `partial` (f32 [ksplit, m, nw * n])
+// is needed when the K split exceeds one block; without it the caller must use
+// another path (returns hipErrorInvalidValue).
+hipError_t run_skinny(const Q4Mat &w, const Q4Mat *w2, const uint16_t *x, uint32_t m, void *out,
+                      const uint16_t *bias, uint32_t ldo, int out_dtype, int accumulate, int act, float *partial,
+                      hipStream_t s) {
+    SkinnyArgs a{};
+    a.w = w;
+    if (w2) a.w2 = *w2;
+    a.x = x;
+    a.m = m;
+    a.k = w.k;
+    a.ldx = w.k;
+    a.out = out;
+    a.bias = bias;
+    a.ldo = ldo;
+    a.act = act;
+    a.out_f32 = out_dtype == KR_DTYPE_F32;
+    a.accumulate = accumulate;
+    const uint32_t ks = skinny_ksplit(w.k);
+    if (ks > 1) {
+        if (!partial) return hipErrorInvalidValue;
+        a.partial = partial;
+    }
+    hipError_t e = launch_skinny(a, s);
+    if (e != hipSuccess || ks == 1) return e;
+    MfmaArgs r{};
+    r.p[0].w = w;
+    r.p[0].out = out;
+    r.p[0].bias = bias;
+    r.p[0].ldo = ldo;
+    r.np = 1;
+    r.m = m;
+    r.act = act;
+    r.out_f32 = a.out_f32;
+    r.accumulate = accumulate;
+    r.partial = partial;
+    r.ksplit = ks;
+    return launch_splitk_reduce(r, w2 ? 2 : 1, s);
+}
+
+bool skinny_fits(uint32_t m, uint32_t k, bool have_partial) {
+    return m >= 2 && m <= kSkinnyMaxM && (have_partial || skinny_ksplit(k) == 1);
+}
+
+size_t partial_bytes(uint32_t m, uint32_t n, uint32_t k, int nw) {
+    const uint32_t ks = std::max<uint32_t>(skinny_ksplit(k), kMaxSplitK);
+    return round_up((size_t)ks * m * nw * n * 4, 256);
+}
+
+// Split K over the blocks when the tile grid alone would leave CUs idle.
+void choose_split_k(MfmaArgs &a, int bm, float *partial) {
+    const uint32_t groups = a.k / 64;
+    const uint32_t rows = (uint32_t)bm_rows(bm);
+    const uint32_t tiles = ((a.m + rows - 1) / rows) * ((a.p[0].w.n + bn_of(bm, false) - 1) / bn_of(bm, false));
+    const uint32_t target = 2u * (uint32_t)device_cus();
+    uint32_t split = 1;
+    while (split < kMaxSplitK && tiles * split < target && groups / (split * 2) >= 8) split *= 2;
+    if (split > 1) {
+        a.ksplit = split;
+        a.groups_per_split = (groups + split - 1) / split;
+        a.partial = partial;
+    }
+}
 
 }  // namespace
 }  // namespace kr
@@ -158,15 +266,19 @@ int kr_q4_linear(const kr_q4_matrix *w, const uint16_t *x, uint32_t m, void *y, 
     if (!aligned(x, 16)) return fail(KR_E_ALIGN, "x must be 16-byte aligned");
     if (!aligned(y, dtype_size(y_dtype))) return fail(KR_E_ALIGN, "y is misaligned for its dtype");
     const Q4Mat a = to_mat(w);
-    const int epi = accumulate ? (y_dtype == KR_DTYPE_F32 ? kAccF32 : kAccBF16)
-                               : (y_dtype == KR_DTYPE_F32 ? kStoreF32 : kStoreBF16);
     hipStream_t s = (hipStream_t)stream;
-    const size_t ysz = dtype_size(y_dtype);
-    for (uint32_t i = 0; i < m; ++i) {
-        hipError_t e = launch_gemv(a, nullptr, x + (size_t)i * w->k, (char *)y + (size_t)i * w->n * ysz, epi, 0, s);
-        if (e != hipSuccess) return hip_status(e, "kr_q4_linear");
+    if (m == 1) {
+        const int epi = accumulate ? (y_dtype == KR_DTYPE_F32 ? kAccF32 : kAccBF16)
+                                   : (y_dtype == KR_DTYPE_F32 ? kStoreF32 : kStoreBF16);
+        return hip_status(launch_gemv(a, nullptr, x, y, epi, 0, nullptr, s), "kr_q4_linear");
     }
-    return ok();
+    if (skinny_fits(m, w->k, false))
+        return hip_status(run_skinny(a, nullptr, x, m, y, nullptr, w->n, y_dtype, accumulate, 0, nullptr, s),
+                          "kr_q4_linear");
+    MfmaArgs args = mfma_args(x, m, w->k, y_dtype, accumulate);
+    args.p[0] = problem(a, nullptr, y, nullptr, w->n);
+    args.np = 1;
+    return hip_status(launch_mfma(args, bm_class(m), s), "kr_q4_linear");
 }
 
 int kr_q4_gate_up_act(const kr_q4_matrix *gate, const kr_q4_matrix *up, const uint16_t *x, uint32_t m,
@@ -182,19 +294,66 @@ int kr_q4_gate_up_act(const kr_q4_matrix *gate, const kr_q4_matrix *up, const ui
     if (!aligned(x, 16)) return fail(KR_E_ALIGN, "x must be 16-byte aligned");
     if (!aligned(act_out, dtype_size(act_dtype))) return fail(KR_E_ALIGN, "act_out misaligned");
     const Q4Mat g = to_mat(gate), u = to_mat(up);
-    const int epi = act_dtype == KR_DTYPE_F32 ? kGateUpF32 : kGateUpBF16;
     hipStream_t s = (hipStream_t)stream;
-    const size_t osz = dtype_size(act_dtype);
-    for (uint32_t i = 0; i < m; ++i) {
-        hipError_t e = launch_gemv(g, &u, x + (size_t)i * gate->k, (char *)act_out + (size_t)i * gate->n * osz, epi,
-                                   activation, s);
-        if (e != hipSuccess) return hip_status(e, "kr_q4_gate_up_act");
+    if (m == 1) {
+        const int epi = act_dtype == KR_DTYPE_F32 ? kGateUpF32 : kGateUpBF16;
+        return hip_status(launch_gemv(g, &u, x, act_out, epi, activation, nullptr, s), "kr_q4_gate_up_act");
     }
-    return ok();
+    if (skinny_fits(m, gate->k, false))
+        return hip_status(run_skinny(g, &u, x, m, act_out, nullptr, gate->n, act_dtype, 0, activation, nullptr, s),
+                          "kr_q4_gate_up_act");
+    MfmaArgs args = mfma_args(x, m, gate->k, act_dtype, 0);
+    args.act = activation;
+    args.p[0] = problem(g, &u, act_out, nullptr, gate->n);
+    args.np = 1;
+    return hip_status(launch_mfma(args, bm_class(m), s), "kr_q4_gate_up_act");
 }
 
-size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t intermediate) {
-    return round_up((size_t)m * intermediate * 2, 256);
+int kr_q4_qkv(const kr_q4_matrix *q, const kr_q4_matrix *k, const kr_q4_matrix *v, const uint16_t *q_bias,
+              const uint16_t *k_bias, const uint16_t *v_bias, const uint16_t *x, uint32_t m, void *q_out,
+              void *k_out, void *v_out, int out_dtype, void *stream) {
+    if (int rc = check_matrix(q, "q")) return rc;
+    if (int rc = check_matrix(k, "k")) return rc;
+    if (int rc = check_matrix(v, "v")) return rc;
+    if (q->k != k->k || q->k != v->k) return fail(KR_E_SHAPE, "q, k, v must share k");
+    if (!valid_dtype(out_dtype)) return fail(KR_E_INVALID, "out_dtype %d invalid", out_dtype);
+    if (m == 0) return ok();
+    if (!x || !q_out || !k_out || !v_out) return fail(KR_E_INVALID, "x and the outputs must be non-NULL");
+    if (!aligned(x, 16)) return fail(KR_E_ALIGN, "x must be 16-byte aligned");
+    const size_t osz = dtype_size(out_dtype);
+    if (!aligned(q_out, osz) || !aligned(k_out, osz) || !aligned(v_out, osz)) return fail(KR_E_ALIGN, "output misaligned");
+    if ((q_bias && !aligned(q_bias, 2)) || (k_bias && !aligned(k_bias, 2)) || (v_bias && !aligned(v_bias, 2)))
+        return fail(KR_E_ALIGN, "bias misaligned");
+    hipStream_t s = (hipStream_t)stream;
+    const kr_q4_matrix *mats[3] = {q, k, v};
+    const uint16_t *biases[3] = {q_bias, k_bias, v_bias};
+    void *outs[3] = {q_out, k_out, v_out};
+    if (m == 1) {
+        const int epi = out_dtype == KR_DTYPE_F32 ? kStoreF32 : kStoreBF16;
+        for (int i = 0; i < 3; ++i) {
+            const hipError_t e = launch_gemv(to_mat(mats[i]), nullptr, x, outs[i], epi, 0, biases[i], s);
+            if (e != hipSuccess) return hip_status(e, "kr_q4_qkv");
+        }
+        return ok();
+    }
+    if (skinny_fits(m, q->k, false)) {
+        for (int i = 0; i < 3; ++i) {
+            const hipError_t e = run_skinny(to_mat(mats[i]), nullptr, x, m, outs[i], biases[i], mats[i]->n, out_dtype,
+                                            0, 0, nullptr, s);
+            if (e != hipSuccess) return hip_status(e, "kr_q4_qkv");
+        }
+        return ok();
+    }
+    MfmaArgs args = mfma_args(x, m, q->k, out_dtype, 0);
+    for (int i = 0; i < 3; ++i) args.p[i] = problem(to_mat(mats[i]), nullptr, outs[i], biases[i], mats[i]->n);
+    args.np = 3;
+    return hip_status(launch_mfma(args, bm_class(m), s), "kr_q4_qkv");
+}
+
+size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermediate) {
+    size_t bytes = round_up((size_t)m * intermediate * 2, 256);
+    if (m > 1) bytes += partial_bytes(m, hidden, intermediate, 1);  // split-K partials of the down projection
+    return bytes;
 }
 
 int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, const uint16_t *x,
@@ -216,13 +375,25 @@ int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matr
     }
     if (!aligned(x, 16)) return fail(KR_E_ALIGN, "x must be 16-byte aligned");
     if (!aligned(h, dtype_size(h_dtype))) return fail(KR_E_ALIGN, "h misaligned");
-    const size_t need = kr_q4_mlp_workspace_bytes(m, gate->n);
+    const size_t need = kr_q4_mlp_workspace_bytes(m, gate->k, gate->n);
     if (!workspace || workspace_bytes < need)
         return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
     if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
     uint16_t *act = (uint16_t *)workspace;
     if (int rc = kr_q4_gate_up_act(gate, up, x, m, act, KR_DTYPE_BF16, activation, stream)) return rc;
-    return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
+    if (m == 1) return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
+    // down projection: few N tiles at small m, so K is split over blocks; partials live in the workspace
+    float *partial = (float *)((char *)workspace + round_up((size_t)m * gate->n * 2, 256));
+    if (skinny_fits(m, down->k, true))
+        return hip_status(run_skinny(to_mat(down), nullptr, act, m, h, nullptr, down->n, h_dtype, 1, 0, partial,
+                                     (hipStream_t)stream),
+                          "kr_q4_mlp (down)");
+    MfmaArgs args = mfma_args(act, m, down->k, h_dtype, 1);
+    args.p[0] = problem(to_mat(down), nullptr, h, nullptr, down->n);
+    args.np = 1;
+    const int bm = bm_class(m);
+    choose_split_k(args, bm, partial);
+    return hip_status(launch_mfma(args, bm, (hipStream_t)stream), "kr_q4_mlp (down)");
 }
 
 }  // extern "C"

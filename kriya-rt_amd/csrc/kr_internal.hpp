@@ -29,6 +29,7 @@ struct Tuning {
     int gemv_persistent_blocks = 1024; // grid of the persistent wave kernel
     int gemv_split_k_chunks = 0;       // rows of >= this many 16-byte chunks use the block kernel
                                        // (always beyond 128 chunks); 0 = default
+    int skinny_max_blocks = 2048;      // grid cap of the few-token kernel (blocks loop over N tiles)
 };
 Tuning &tuning();
 
@@ -41,8 +42,57 @@ hipError_t launch_from_blocks36(const void *blocks, uint32_t n, uint32_t k, uint
 hipError_t launch_to_blocks36(const Q4Mat &w, void *blocks, hipStream_t s);
 hipError_t launch_f16_to_bf16(const uint16_t *in, uint16_t *out, size_t count, hipStream_t s);
 
-// y = W x for one token; `b` is the up matrix for the gate/up epilogues.
+// ---- batched (m > 1) matrix-core path (q4_mfma.hip)
+constexpr int kMaxMfmaProblems = 3;
+enum MfmaEpilogue : int { kMfmaDirect = 0, kMfmaPartial = 1 };
+
+struct MfmaProblem {
+    Q4Mat w;                // N = w.n rows, k = MfmaArgs::k
+    Q4Mat w2;               // up matrix for the gate/up epilogue (qw == nullptr otherwise)
+    void *out;              // [m, ldo] bf16 or f32
+    const uint16_t *bias;   // bf16 [N] added before the store, or nullptr
+    uint32_t ldo;           // output row stride in elements
+    uint32_t tile_begin;    // set by the launcher
+};
+
+struct MfmaArgs {
+    MfmaProblem p[kMaxMfmaProblems];
+    int np;
+    const uint16_t *x;      // bf16 [m, ldx]
+    uint32_t m, k, ldx;
+    int act;                // activation of the gate/up epilogue
+    int out_f32;            // 1: f32 outputs, 0: bf16
+    int accumulate;         // 1: out += result (bf16: RNE of the f32 sum)
+    float *partial;         // split-K partials [ksplit, m, nw * N] (ksplit > 1)
+    uint32_t ksplit;
+    uint32_t groups_per_split;
+};
+
+// bm: the M tile class (16, 64 or 128) chosen by the caller from m.
+hipError_t launch_mfma(MfmaArgs &a, int bm, hipStream_t s);
+// Fixed-order sum of split-K partials [ksplit, m, nw * N] + the epilogue of p[0].
+hipError_t launch_splitk_reduce(const MfmaArgs &a, int nw, hipStream_t s);
+
+// ---- few-token (m <= 16) matrix-core path (q4_skinny.hip)
+constexpr uint32_t kSkinnyMaxM = 16;
+struct SkinnyArgs {
+    Q4Mat w, w2;            // w2: up matrix for the gate/up epilogue (qw == nullptr otherwise)
+    const uint16_t *x;      // bf16 [m, ldx]
+    uint32_t m, k, ldx;
+    void *out;              // [m, ldo]
+    const uint16_t *bias;   // bf16 [n] or nullptr
+    uint32_t ldo;
+    int act, out_f32, accumulate;
+    float *partial;         // [ksplit, m, nw * n] when the K split exceeds one block, else nullptr
+    uint32_t ksplit;        // set by the launcher
+};
+hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s);
+// Number of K splits (blocks per N tile) the skinny launcher uses for rows of k columns.
+uint32_t skinny_ksplit(uint32_t k);
+
+// y = W x for one token; `b` is the up matrix for the gate/up epilogues;
+// `bias` (bf16 [n] or nullptr) is added by the store epilogues.
 hipError_t launch_gemv(const Q4Mat &a, const Q4Mat *b, const uint16_t *x, void *out, int epilogue,
-                       int activation, hipStream_t s);
+                       int activation, const uint16_t *bias, hipStream_t s);
 
 }  // namespace kr

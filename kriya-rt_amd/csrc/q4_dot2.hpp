@@ -68,8 +68,19 @@ __device__ __forceinline__ float chunk_dot(const u32x4 &wv, uint32_t sraw, uint3
     return fmaf(s, d, fmaf(fmaf(-128.0f, s, b), xc.sum, acc));
 }
 
+// Epilogue operands of the m == 1 kernels.
+struct GemvOut {
+    void *out;              // [n] (or [channels] for gate/up)
+    const uint16_t *bias;   // bf16 [n] added by the store epilogues, or nullptr
+    int act;                // activation of the gate/up epilogues
+};
+
 template <int EPI>
-__device__ __forceinline__ void store_row(void *out, uint32_t row, float v) {
+__device__ __forceinline__ void store_row(const GemvOut &o, uint32_t row, float v) {
+    void *out = o.out;
+    if (EPI == kStoreF32 || EPI == kStoreBF16) {
+        if (o.bias) v += bf16_to_f32(o.bias[row]);
+    }
     if (EPI == kStoreF32) {
         reinterpret_cast<float *>(out)[row] = v;
     } else if (EPI == kStoreBF16) {
@@ -109,7 +120,7 @@ __device__ __forceinline__ void tile_rows(const Q4Mat &A, const Q4Mat &B, uint32
 }
 
 template <int R, int EPI>
-__device__ __forceinline__ void tile_epilogue(float tot, int lane, uint32_t t, uint32_t nrows, void *out, int act) {
+__device__ __forceinline__ void tile_epilogue(float tot, int lane, uint32_t t, uint32_t nrows, const GemvOut &o) {
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
     constexpr int kSeg = kWave / R;
     const int slot = lane / kSeg;
@@ -117,11 +128,11 @@ __device__ __forceinline__ void tile_epilogue(float tot, int lane, uint32_t t, u
         const float up = __shfl_xor(tot, kSeg);
         if ((lane % kSeg) == 0 && (slot & 1) == 0) {
             const uint32_t ch = t * (R / 2) + (slot >> 1);
-            if (ch < nrows) store_row<EPI>(out, ch, activation(tot, act) * up);
+            if (ch < nrows) store_row<EPI>(o, ch, activation(tot, o.act) * up);
         }
     } else if ((lane % kSeg) == 0) {
         const uint32_t row = t * R + slot;
-        if (row < nrows) store_row<EPI>(out, row, tot);
+        if (row < nrows) store_row<EPI>(o, row, tot);
     }
 }
 

@@ -34,7 +34,7 @@ namespace kr {
 
 template <int R, int C, int EPI>
 __global__ __launch_bounds__(256) void q4_gemv_wave_kernel(Q4Mat A, Q4Mat B, const uint16_t *__restrict__ x,
-                                                           void *__restrict__ out, int act, uint32_t tiles) {
+                                                           GemvOut o, uint32_t tiles) {
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
     const int lane = threadIdx.x & (kWave - 1);
     const uint32_t nwaves = gridDim.x * 4;
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void q4_gemv_wave_kernel(Q4Mat A, Q4Mat B, con
         const uint32_t tn = t + nwaves;
         if (tn < tiles) fetch(tn);
         const float tot = wave_reduce_rows<R>(acc, lane);
-        tile_epilogue<R, EPI>(tot, lane, t, A.n, out, act);
+        tile_epilogue<R, EPI>(tot, lane, t, A.n, o);
         if (tn >= tiles) break;
         t = tn;
     }
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void q4_gemv_wave_kernel(Q4Mat A, Q4Mat B, con
 
 template <int R, int C, int EPI>
 __global__ __launch_bounds__(256) void q4_gemv_block_kernel(Q4Mat A, Q4Mat B, const uint16_t *__restrict__ x,
-                                                            void *__restrict__ out, int act, uint32_t tiles) {
+                                                            GemvOut o, uint32_t tiles) {
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
     constexpr int kSeg = kWave / R;
     __shared__ float red[4][R];
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void q4_gemv_block_kernel(Q4Mat A, Q4Mat B, co
         __syncthreads();
         if (wave == 0) {
             tot = ((red[0][slot] + red[1][slot]) + red[2][slot]) + red[3][slot];
-            tile_epilogue<R, EPI>(tot, lane, t, A.n, out, act);
+            tile_epilogue<R, EPI>(tot, lane, t, A.n, o);
         }
         if (tn >= tiles) break;
         __syncthreads();  // red is rewritten by the next tile
@@ -189,33 +189,32 @@ static uint32_t cap_blocks(uint32_t blocks, uint32_t persistent_default) {
 }
 
 template <int R, int EPI>
-static hipError_t launch_wave(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, void *out, int act, hipStream_t s) {
+static hipError_t launch_wave(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, const GemvOut &o, hipStream_t s) {
     const uint32_t tiles = tiles_for<EPI>(a.n, R);
     const uint32_t blocks = cap_blocks((tiles + 3) / 4, (uint32_t)tuning().gemv_persistent_blocks);
     if (a.k <= 64 * 32)
-        hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 1, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, out, act, tiles);
+        hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 1, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, o, tiles);
     else
-        hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 2, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, out, act, tiles);
+        hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 2, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, o, tiles);
     return hipGetLastError();
 }
 
 template <int R, int EPI>
-static hipError_t launch_block(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, void *out, int act,
-                               hipStream_t s) {
+static hipError_t launch_block(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, const GemvOut &o, hipStream_t s) {
     const uint32_t tiles = tiles_for<EPI>(a.n, R);
     const uint32_t blocks = cap_blocks(tiles, 1u << 30);
     const uint32_t nchunks = a.k >> 5;
     if (nchunks <= 256)
-        hipLaunchKernelGGL((q4_gemv_block_kernel<R, 1, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, out, act, tiles);
+        hipLaunchKernelGGL((q4_gemv_block_kernel<R, 1, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, o, tiles);
     else if (nchunks <= 512)
-        hipLaunchKernelGGL((q4_gemv_block_kernel<R, 2, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, out, act, tiles);
+        hipLaunchKernelGGL((q4_gemv_block_kernel<R, 2, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, o, tiles);
     else
-        hipLaunchKernelGGL((q4_gemv_block_kernel<R, 3, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, out, act, tiles);
+        hipLaunchKernelGGL((q4_gemv_block_kernel<R, 3, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, o, tiles);
     return hipGetLastError();
 }
 
 template <int EPI>
-static hipError_t launch_epi(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, void *out, int act, hipStream_t s) {
+static hipError_t launch_epi(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, const GemvOut &o, hipStream_t s) {
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
     const uint32_t chunks = a.k >> 5;
     const int split = tuning().gemv_split_k_chunks;
@@ -224,28 +223,29 @@ static hipError_t launch_epi(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, 
     switch (rw) {
         case 1:
             if constexpr (!kGateUp)
-                return use_block ? launch_block<1, EPI>(a, b, x, out, act, s) : launch_wave<1, EPI>(a, b, x, out, act, s);
+                return use_block ? launch_block<1, EPI>(a, b, x, o, s) : launch_wave<1, EPI>(a, b, x, o, s);
             else
-                return use_block ? launch_block<2, EPI>(a, b, x, out, act, s) : launch_wave<2, EPI>(a, b, x, out, act, s);
+                return use_block ? launch_block<2, EPI>(a, b, x, o, s) : launch_wave<2, EPI>(a, b, x, o, s);
         case 2:
-            return use_block ? launch_block<2, EPI>(a, b, x, out, act, s) : launch_wave<2, EPI>(a, b, x, out, act, s);
+            return use_block ? launch_block<2, EPI>(a, b, x, o, s) : launch_wave<2, EPI>(a, b, x, o, s);
         case 8:
-            return use_block ? launch_block<8, EPI>(a, b, x, out, act, s) : launch_wave<8, EPI>(a, b, x, out, act, s);
+            return use_block ? launch_block<8, EPI>(a, b, x, o, s) : launch_wave<8, EPI>(a, b, x, o, s);
         default:
-            return use_block ? launch_block<4, EPI>(a, b, x, out, act, s) : launch_wave<4, EPI>(a, b, x, out, act, s);
+            return use_block ? launch_block<4, EPI>(a, b, x, o, s) : launch_wave<4, EPI>(a, b, x, o, s);
     }
 }
 
 hipError_t launch_gemv(const Q4Mat &a, const Q4Mat *b, const uint16_t *x, void *out, int epilogue, int act,
-                       hipStream_t s) {
+                       const uint16_t *bias, hipStream_t s) {
     const Q4Mat &bb = b ? *b : a;
+    const GemvOut o{out, bias, act};
     switch (epilogue) {
-        case kStoreF32: return launch_epi<kStoreF32>(a, bb, x, out, act, s);
-        case kStoreBF16: return launch_epi<kStoreBF16>(a, bb, x, out, act, s);
-        case kAccF32: return launch_epi<kAccF32>(a, bb, x, out, act, s);
-        case kAccBF16: return launch_epi<kAccBF16>(a, bb, x, out, act, s);
-        case kGateUpF32: return launch_epi<kGateUpF32>(a, bb, x, out, act, s);
-        case kGateUpBF16: return launch_epi<kGateUpBF16>(a, bb, x, out, act, s);
+        case kStoreF32: return launch_epi<kStoreF32>(a, bb, x, o, s);
+        case kStoreBF16: return launch_epi<kStoreBF16>(a, bb, x, o, s);
+        case kAccF32: return launch_epi<kAccF32>(a, bb, x, o, s);
+        case kAccBF16: return launch_epi<kAccBF16>(a, bb, x, o, s);
+        case kGateUpF32: return launch_epi<kGateUpF32>(a, bb, x, o, s);
+        case kGateUpBF16: return launch_epi<kGateUpBF16>(a, bb, x, o, s);
         default: return hipErrorInvalidValue;
     }
 }

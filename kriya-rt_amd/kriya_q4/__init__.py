@@ -68,7 +68,8 @@ def lib():
             "kr_f16_to_bf16": (i32, [vp, vp, sz, vp]),
             "kr_q4_linear": (i32, [M, vp, u32, vp, i32, i32, vp]),
             "kr_q4_gate_up_act": (i32, [M, M, vp, u32, vp, i32, i32, vp]),
-            "kr_q4_mlp_workspace_bytes": (sz, [u32, u32]),
+            "kr_q4_mlp_workspace_bytes": (sz, [u32, u32, u32]),
+            "kr_q4_qkv": (i32, [M, M, M, vp, vp, vp, vp, u32, vp, vp, vp, i32, vp]),
             "kr_q4_mlp": (i32, [M, M, M, vp, vp, i32, u32, i32, vp, sz, vp]),
         }
         for name, (res, args) in sig.items():
@@ -198,13 +199,24 @@ def gate_up_act(gate: Q4Matrix, up: Q4Matrix, x: torch.Tensor, out: Optional[tor
     return out
 
 
-def mlp_workspace_bytes(m: int, intermediate: int) -> int:
-    return int(lib().kr_q4_mlp_workspace_bytes(m, intermediate))
+def mlp_workspace_bytes(m: int, hidden: int, intermediate: int) -> int:
+    return int(lib().kr_q4_mlp_workspace_bytes(m, hidden, intermediate))
 
 
-def mlp_workspace(m: int, intermediate: int, device="cuda") -> torch.Tensor:
-    """Device workspace of an MLP call (the bf16 intermediate)."""
-    return torch.empty(mlp_workspace_bytes(m, intermediate), dtype=torch.uint8, device=device)
+def mlp_workspace(m: int, hidden: int, intermediate: int, device="cuda") -> torch.Tensor:
+    """Device workspace of an MLP call (bf16 intermediate + split-K partials)."""
+    return torch.empty(mlp_workspace_bytes(m, hidden, intermediate), dtype=torch.uint8, device=device)
+
+
+def qkv(q: Q4Matrix, k: Q4Matrix, v: Q4Matrix, x: torch.Tensor, q_bias=None, k_bias=None, v_bias=None,
+        out_dtype: int = DTYPE_F32, outs=None, stream=None):
+    """(x q^T + q_bias, x k^T + k_bias, x v^T + v_bias) for x bf16 [m, hidden]."""
+    m = x.numel() // q.k
+    if outs is None:
+        outs = tuple(torch.empty((m, w.n), dtype=_out_dtype(out_dtype), device=x.device) for w in (q, k, v))
+    _check(lib().kr_q4_qkv(q.desc, k.desc, v.desc, _ptr(q_bias), _ptr(k_bias), _ptr(v_bias), _ptr(x), m,
+                           _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]), _dt_of(outs[0]), _stream(stream)))
+    return outs
 
 
 def mlp(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, h: torch.Tensor, x: Optional[torch.Tensor] = None,
@@ -212,7 +224,7 @@ def mlp(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, h: torch.Tensor, x: Option
     """h += down(act(gate x) * (up x)) in place; x defaults to h (bf16 h)."""
     m = h.numel() // down.n
     if workspace is None:
-        workspace = mlp_workspace(m, gate.n, device=h.device)
+        workspace = mlp_workspace(m, gate.k, gate.n, device=h.device)
     _check(lib().kr_q4_mlp(gate.desc, up.desc, down.desc, _ptr(x), _ptr(h), _dt_of(h), m, activation,
                            _ptr(workspace), workspace.numel(), _stream(stream)))
     return h

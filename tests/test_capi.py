@@ -81,8 +81,8 @@ def test_gate_up_and_mlp_argument_checks(kq):
     x, out = 0x40000, 0x50000
     assert L.kr_q4_gate_up_act(ctypes.byref(g), ctypes.byref(bad_u), x, 1, out, 0, 0, None) == kq.KR_E_SHAPE
     assert L.kr_q4_gate_up_act(ctypes.byref(g), ctypes.byref(u), x, 1, out, 0, 9, None) == kq.KR_E_INVALID
-    need = L.kr_q4_mlp_workspace_bytes(4, 192)
-    assert need >= 4 * 192 * 2 and need % 256 == 0
+    need = L.kr_q4_mlp_workspace_bytes(4, 128, 192)
+    assert need >= 4 * 192 * 2 + 4 * 128 * 4 and need % 256 == 0
     rc = L.kr_q4_mlp(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), x, out, 0, 4, 0, 0x60000, need - 1, None)
     assert rc == kq.KR_E_WORKSPACE
     rc = L.kr_q4_mlp(ctypes.byref(g), ctypes.byref(u), ctypes.byref(bad_u), x, out, 0, 4, 0, 0x60000, need, None)

