@@ -81,6 +81,9 @@ const char *kr_last_error(void);
                                            0 (default): only beyond k = 4096               */
 #define KR_OPT_GEMV_BLOCK_ROWS 4        /* rows per split-K block tile: 1, 2 (default), 4, 8 */
 #define KR_OPT_GEMV_PERSISTENT_BLOCKS 5 /* grid of the persistent wave kernel (1024)       */
+#define KR_OPT_SKINNY_MAX_BLOCKS 6      /* grid cap of the few-token kernel (512)          */
+#define KR_OPT_SKINNY_LANE_COLS 7       /* few-token kernel: columns per lane group, 64 or 128 (128) */
+#define KR_OPT_SKINNY_WAVES 8           /* few-token kernel: waves per block, 4 (default) or 8 */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 
@@ -154,6 +157,56 @@ size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermedi
 int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down,
               const uint16_t *x, void *h, int h_dtype, uint32_t m, int activation,
               void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- MoE routing: q4_gemm_and_moe.metal:2495-2624 (moe_router_topk_and_histogram
+ *      + moe_router_prefix_scan_and_scatter, dispatched at encoder.rs:5275-5313) ----
+ * logits: f32 [tokens, experts].  Per token: softmax, then the top `topk`
+ * probabilities by insertion with strict '>' (ties go to the lower expert id),
+ * renormalised by their sum (floored at 1e-8) when normalize != 0.
+ * Outputs (device):
+ *   selected      u32 [tokens, topk]  expert ids, descending probability
+ *   weights       f32 [tokens, topk]
+ *   counts        u32 [experts]
+ *   offsets       u32 [experts + 1]   exclusive prefix sum of counts
+ *   sorted_assign u32 [tokens * topk] assignment ids a = t * topk + k grouped by
+ *                 expert: bucket e is sorted_assign[offsets[e] .. offsets[e+1]),
+ *                 increasing a inside a bucket.
+ * Deterministic (the reference's bucket order depends on atomic timing).
+ * Limits: experts <= 256, topk <= min(experts, 16), tokens * topk <= 16384. */
+int kr_moe_route(const float *logits, uint32_t tokens, uint32_t experts, uint32_t topk, int normalize,
+                 uint32_t *selected, float *weights, uint32_t *counts, uint32_t *offsets,
+                 uint32_t *sorted_assign, void *stream);
+
+/* The scan/scatter stage alone (q4_gemm_and_moe.metal:2578-2624) for given
+ * assignments selected[num_assign]: counts, offsets and sorted_assign as above.
+ * An id >= experts joins no bucket, so offsets[experts] < num_assign reports it.
+ * Limits: experts <= 256, num_assign <= 16384. */
+int kr_moe_scan_scatter(const uint32_t *selected, uint32_t num_assign, uint32_t experts,
+                        uint32_t *counts, uint32_t *offsets, uint32_t *sorted_assign, void *stream);
+
+/* ---- routed Q4 experts + combine: encoder.rs:5316-5445 (q4_g64_routed_moe_gemv
+ *      for gate, up and down, q4_gemm_and_moe.metal:2642-2698;
+ *      fused_gated_activation_bf16 and moe_combine_routed_and_shared_bf16,
+ *      transformer_glue.metal:307-336, 373-401) ----
+ * gate, up: `experts` stacked matrices, n = experts * inter, k = hidden
+ * (expert e owns rows e*inter .. (e+1)*inter); down: n = experts * hidden, k = inter.
+ * For each assignment a = t * topk + k with expert e:
+ *   h_a = bf16(act(gate_e . x_t) * (up_e . x_t)),   d_a = down_e . h_a  (f32),
+ *   y[t] = sum over k = 0 .. topk-1 of fma(weights[a], d_a, acc), in slot order,
+ * stored as y_dtype; accumulate = 1 adds it to y as kr_q4_linear does.
+ * offsets and sorted_assign are kr_moe_route's.  Every expert's weights are read
+ * once per call for all the tokens routed to it (grouped matmul; the reference
+ * re-reads them per routed token).  The reference also rounds gate.x, up.x and
+ * d_a to bf16; here they stay f32.
+ * workspace: kr_q4_moe_workspace_bytes(tokens, topk, hidden, inter) bytes,
+ * 16-byte aligned; calls sharing it must not overlap in time.
+ * Limits: experts <= 256; hidden and inter <= 2048, or <= 4096 when a multiple of 128. */
+size_t kr_q4_moe_workspace_bytes(uint32_t tokens, uint32_t topk, uint32_t hidden, uint32_t inter);
+int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down,
+                      uint32_t experts, const uint16_t *x, uint32_t tokens, uint32_t topk,
+                      const float *weights, const uint32_t *offsets, const uint32_t *sorted_assign,
+                      int activation, void *y, int y_dtype, int accumulate,
+                      void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -155,7 +155,10 @@ bool skinny_fits(uint32_t m, uint32_t k, bool have_partial) {
 }
 
 size_t partial_bytes(uint32_t m, uint32_t n, uint32_t k, int nw) {
-    const uint32_t ks = std::max<uint32_t>(skinny_ksplit(k), kMaxSplitK);
+    // the largest K split of any skinny launch shape (64-column lane groups, 4 waves), so that
+    // a workspace sized once stays valid under every tuning option
+    const uint32_t skinny_worst = ((k + 255) / 256 + 3) / 4;
+    const uint32_t ks = std::max<uint32_t>(skinny_worst, kMaxSplitK);
     return round_up((size_t)ks * m * nw * n * 4, 256);
 }
 
@@ -209,6 +212,18 @@ int kr_set_option(int option, int value) {
             if (value < 1) return fail(KR_E_INVALID, "persistent blocks must be >= 1");
             tuning().gemv_persistent_blocks = value;
             return ok();
+        case KR_OPT_SKINNY_MAX_BLOCKS:
+            if (value < 1) return fail(KR_E_INVALID, "skinny max blocks must be >= 1");
+            tuning().skinny_max_blocks = value;
+            return ok();
+        case KR_OPT_SKINNY_LANE_COLS:
+            if (value != 64 && value != 128) return fail(KR_E_INVALID, "skinny lane columns must be 64 or 128");
+            tuning().skinny_lane_cols = value;
+            return ok();
+        case KR_OPT_SKINNY_WAVES:
+            if (value != 4 && value != 8) return fail(KR_E_INVALID, "skinny waves must be 4 or 8");
+            tuning().skinny_waves = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -220,6 +235,9 @@ int kr_get_option(int option) {
         case KR_OPT_GEMV_SPLIT_K_CHUNKS: return tuning().gemv_split_k_chunks;
         case KR_OPT_GEMV_BLOCK_ROWS: return tuning().gemv_block_rows;
         case KR_OPT_GEMV_PERSISTENT_BLOCKS: return tuning().gemv_persistent_blocks;
+        case KR_OPT_SKINNY_MAX_BLOCKS: return tuning().skinny_max_blocks;
+        case KR_OPT_SKINNY_LANE_COLS: return tuning().skinny_lane_cols;
+        case KR_OPT_SKINNY_WAVES: return tuning().skinny_waves;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -394,6 +412,118 @@ int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matr
     const int bm = bm_class(m);
     choose_split_k(args, bm, partial);
     return hip_status(launch_mfma(args, bm, (hipStream_t)stream), "kr_q4_mlp (down)");
+}
+
+int kr_moe_route(const float *logits, uint32_t tokens, uint32_t experts, uint32_t topk, int normalize,
+                 uint32_t *selected, float *weights, uint32_t *counts, uint32_t *offsets, uint32_t *sorted_assign,
+                 void *stream) {
+    if (experts == 0 || experts > kMaxExperts) return fail(KR_E_INVALID, "experts=%u must be in 1..%u", experts, kMaxExperts);
+    if (topk == 0 || topk > experts || topk > kRouteMaxTopK)
+        return fail(KR_E_INVALID, "topk=%u must be in 1..min(experts, %u)", topk, kRouteMaxTopK);
+    if ((uint64_t)tokens * topk > kRouteMaxAssign)
+        return fail(KR_E_SHAPE, "tokens * topk = %llu exceeds %u", (unsigned long long)tokens * topk, kRouteMaxAssign);
+    if (!counts || !offsets) return fail(KR_E_INVALID, "counts/offsets must be non-NULL");
+    if (tokens > 0 && (!logits || !selected || !weights || !sorted_assign))
+        return fail(KR_E_INVALID, "logits/selected/weights/sorted_assign must be non-NULL");
+    if (!aligned(logits, 4) || !aligned(selected, 4) || !aligned(weights, 4) || !aligned(counts, 4) ||
+        !aligned(offsets, 4) || !aligned(sorted_assign, 4))
+        return fail(KR_E_ALIGN, "routing arrays must be 4-byte aligned");
+    return hip_status(launch_moe_route(tokens ? logits : nullptr, tokens, experts, topk, normalize, selected, weights,
+                                       counts, offsets, sorted_assign, (hipStream_t)stream),
+                      "kr_moe_route");
+}
+
+int kr_moe_scan_scatter(const uint32_t *selected, uint32_t num_assign, uint32_t experts, uint32_t *counts,
+                        uint32_t *offsets, uint32_t *sorted_assign, void *stream) {
+    if (experts == 0 || experts > kMaxExperts) return fail(KR_E_INVALID, "experts=%u must be in 1..%u", experts, kMaxExperts);
+    if (num_assign > kRouteMaxAssign) return fail(KR_E_SHAPE, "num_assign=%u exceeds %u", num_assign, kRouteMaxAssign);
+    if (!counts || !offsets) return fail(KR_E_INVALID, "counts/offsets must be non-NULL");
+    if (num_assign > 0 && (!selected || !sorted_assign))
+        return fail(KR_E_INVALID, "selected/sorted_assign must be non-NULL");
+    if (!aligned(selected, 4) || !aligned(counts, 4) || !aligned(offsets, 4) || !aligned(sorted_assign, 4))
+        return fail(KR_E_ALIGN, "routing arrays must be 4-byte aligned");
+    // the kernel's given-assignment mode: T = num_assign rows of one slot each
+    return hip_status(launch_moe_route(nullptr, num_assign, experts, 1, 0, const_cast<uint32_t *>(selected), nullptr,
+                                       counts, offsets, sorted_assign, (hipStream_t)stream),
+                      "kr_moe_scan_scatter");
+}
+
+size_t kr_q4_moe_workspace_bytes(uint32_t tokens, uint32_t topk, uint32_t hidden, uint32_t inter) {
+    const size_t assign = (size_t)tokens * topk;
+    return round_up(assign * inter * 2, 256) + round_up(assign * hidden * 4, 256);
+}
+
+int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, uint32_t experts,
+                      const uint16_t *x, uint32_t tokens, uint32_t topk, const float *weights, const uint32_t *offsets,
+                      const uint32_t *sorted_assign, int activation, void *y, int y_dtype, int accumulate,
+                      void *workspace, size_t workspace_bytes, void *stream) {
+    if (int rc = check_matrix(gate, "gate")) return rc;
+    if (int rc = check_matrix(up, "up")) return rc;
+    if (int rc = check_matrix(down, "down")) return rc;
+    if (experts == 0 || experts > kMaxExperts) return fail(KR_E_INVALID, "experts=%u must be in 1..%u", experts, kMaxExperts);
+    if (gate->n != up->n || gate->k != up->k) return fail(KR_E_SHAPE, "gate and up shapes differ");
+    if (gate->n % experts != 0) return fail(KR_E_SHAPE, "gate rows %u are not a multiple of experts=%u", gate->n, experts);
+    const uint32_t hidden = gate->k, inter = gate->n / experts;
+    if (down->k != inter || down->n != experts * hidden)
+        return fail(KR_E_SHAPE, "down [%u,%u] does not stack %u experts of [%u,%u]", down->n, down->k, experts, hidden,
+                    inter);
+    if (!skinny_grouped_fits(hidden) || !skinny_grouped_fits(inter))
+        return fail(KR_E_UNSUPPORTED, "hidden=%u / inter=%u: rows longer than one block covers", hidden, inter);
+    if (topk == 0 || topk > experts) return fail(KR_E_INVALID, "topk=%u must be in 1..experts", topk);
+    if (!valid_dtype(y_dtype)) return fail(KR_E_INVALID, "y_dtype %d invalid", y_dtype);
+    if (!valid_act(activation)) return fail(KR_E_INVALID, "activation %d invalid", activation);
+    if (accumulate != 0 && accumulate != 1) return fail(KR_E_INVALID, "accumulate must be 0 or 1");
+    if (tokens == 0) return ok();
+    if ((uint64_t)tokens * topk > 0xFFFFFFFFull / 2) return fail(KR_E_SHAPE, "too many assignments");
+    if (!x || !weights || !offsets || !sorted_assign || !y) return fail(KR_E_INVALID, "NULL pointer");
+    if (!aligned(x, 16)) return fail(KR_E_ALIGN, "x must be 16-byte aligned");
+    if (!aligned(y, dtype_size(y_dtype) * 4)) return fail(KR_E_ALIGN, "y must be aligned to 4 elements");
+    if (!aligned(weights, 4) || !aligned(offsets, 4) || !aligned(sorted_assign, 4))
+        return fail(KR_E_ALIGN, "routing arrays must be 4-byte aligned");
+    const size_t need = kr_q4_moe_workspace_bytes(tokens, topk, hidden, inter);
+    if (!workspace || workspace_bytes < need)
+        return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    const uint32_t assign = tokens * topk;
+    uint16_t *h = (uint16_t *)workspace;                                              // [assign, inter] bf16, sorted order
+    float *d = (float *)((char *)workspace + round_up((size_t)assign * inter * 2, 256));  // [assign, hidden] f32
+
+    SkinnyArgs g{};
+    g.w = to_mat(gate);
+    g.w2 = to_mat(up);
+    g.x = x;
+    g.k = hidden;
+    g.ldx = hidden;
+    g.out = h;
+    g.ldo = inter;
+    g.act = activation;
+    g.offsets = offsets;
+    g.sorted = sorted_assign;
+    g.experts = experts;
+    g.expert_rows = inter;
+    g.x_div = topk;  // X row of an assignment = its token
+    g.max_active = std::min(experts, assign);
+    if (hipError_t e = launch_skinny(g, s)) return hip_status(e, "kr_q4_moe_experts (gate/up)");
+
+    SkinnyArgs dn{};
+    dn.w = to_mat(down);
+    dn.x = h;
+    dn.k = inter;
+    dn.ldx = inter;
+    dn.out = d;
+    dn.ldo = hidden;
+    dn.out_f32 = 1;
+    dn.offsets = offsets;
+    dn.sorted = sorted_assign;
+    dn.experts = experts;
+    dn.expert_rows = hidden;
+    dn.out_scatter = 1;  // result rows back in assignment order
+    dn.max_active = g.max_active;
+    if (hipError_t e = launch_skinny(dn, s)) return hip_status(e, "kr_q4_moe_experts (down)");
+
+    return hip_status(launch_moe_combine(d, weights, tokens, topk, hidden, y, y_dtype == KR_DTYPE_F32, accumulate, s),
+                      "kr_q4_moe_experts (combine)");
 }
 
 }  // extern "C"

@@ -29,7 +29,9 @@ struct Tuning {
     int gemv_persistent_blocks = 1024; // grid of the persistent wave kernel
     int gemv_split_k_chunks = 0;       // rows of >= this many 16-byte chunks use the block kernel
                                        // (always beyond 128 chunks); 0 = default
-    int skinny_max_blocks = 2048;      // grid cap of the few-token kernel (blocks loop over N tiles)
+    int skinny_max_blocks = 512;       // grid cap of the few-token kernel (blocks walk runs of tiles)
+    int skinny_lane_cols = 128;        // few-token kernel: columns per lane group (64 or 128)
+    int skinny_waves = 4;              // few-token kernel: K ranges (waves) per block (4 or 8)
 };
 Tuning &tuning();
 
@@ -73,22 +75,43 @@ hipError_t launch_mfma(MfmaArgs &a, int bm, hipStream_t s);
 // Fixed-order sum of split-K partials [ksplit, m, nw * N] + the epilogue of p[0].
 hipError_t launch_splitk_reduce(const MfmaArgs &a, int nw, hipStream_t s);
 
-// ---- few-token (m <= 16) matrix-core path (q4_skinny.hip)
+// ---- few-token (m <= 16) and grouped MoE matrix-core path (q4_skinny.hip)
 constexpr uint32_t kSkinnyMaxM = 16;
+constexpr uint32_t kMaxExperts = 256;
 struct SkinnyArgs {
     Q4Mat w, w2;            // w2: up matrix for the gate/up epilogue (qw == nullptr otherwise)
-    const uint16_t *x;      // bf16 [m, ldx]
-    uint32_t m, k, ldx;
-    void *out;              // [m, ldo]
-    const uint16_t *bias;   // bf16 [n] or nullptr
+    const uint16_t *x;      // bf16 [rows, ldx]
+    uint32_t m, k, ldx;     // m: token rows (dense mode)
+    void *out;              // [rows, ldo]
+    const uint16_t *bias;   // bf16 [n] or nullptr (dense mode)
     uint32_t ldo;
     int act, out_f32, accumulate;
     float *partial;         // [ksplit, m, nw * n] when the K split exceeds one block, else nullptr
     uint32_t ksplit;        // set by the launcher
+    // grouped (MoE) mode; offsets == nullptr selects dense mode
+    const uint32_t *offsets;  // [experts + 1] bucket offsets into `sorted`
+    const uint32_t *sorted;   // expert-sorted assignment ids
+    uint32_t experts;         // E; w (and w2) stack E matrices of expert_rows rows
+    uint32_t expert_rows;
+    uint32_t x_div;           // > 0: X row of sorted position p is sorted[p] / x_div; 0: row p
+    int out_scatter;          // 1: result row of sorted position p goes to row sorted[p]; 0: row p
+    uint32_t max_active;      // upper bound of non-empty buckets (sizes the grid)
 };
 hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s);
-// Number of K splits (blocks per N tile) the skinny launcher uses for rows of k columns.
+
+// ---- MoE routing and combine (moe.hip)
+constexpr uint32_t kRouteMaxTopK = 16;      // top-k list length of the routing kernel
+constexpr uint32_t kRouteMaxAssign = 16384; // T * K held in the routing block's LDS
+// logits == nullptr: `experts` [T*K] are given and only counts/offsets/sorted are produced.
+hipError_t launch_moe_route(const float *logits, uint32_t T, uint32_t E, uint32_t K, int normalize,
+                            uint32_t *experts, float *weights, uint32_t *counts, uint32_t *offsets, uint32_t *sorted,
+                            hipStream_t s);
+hipError_t launch_moe_combine(const float *d, const float *w, uint32_t T, uint32_t K, uint32_t H, void *y, int y_f32,
+                              int accumulate, hipStream_t s);
+// Number of K splits (blocks per N tile) the dense skinny launcher uses for rows of k columns.
 uint32_t skinny_ksplit(uint32_t k);
+// True when one block of the grouped kernel covers rows of k columns (no K split).
+bool skinny_grouped_fits(uint32_t k);
 
 // y = W x for one token; `b` is the up matrix for the gate/up epilogues;
 // `bias` (bf16 [n] or nullptr) is added by the store epilogues.

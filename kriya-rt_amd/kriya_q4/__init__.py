@@ -28,7 +28,8 @@ KR_E_INVALID, KR_E_SHAPE, KR_E_ALIGN, KR_E_HIP, KR_E_WORKSPACE, KR_E_UNSUPPORTED
 DTYPE_BF16, DTYPE_F32 = 0, 1
 ACT_SWIGLU, ACT_GEGLU, ACT_RELU = 0, 1, 2
 OPT_GEMV_ROWS_PER_WAVE, OPT_GEMV_MAX_BLOCKS, OPT_GEMV_SPLIT_K_CHUNKS = 1, 2, 3
-OPT_GEMV_BLOCK_ROWS, OPT_GEMV_PERSISTENT_BLOCKS = 4, 5
+OPT_GEMV_BLOCK_ROWS, OPT_GEMV_PERSISTENT_BLOCKS, OPT_SKINNY_MAX_BLOCKS = 4, 5, 6
+OPT_SKINNY_LANE_COLS, OPT_SKINNY_WAVES = 7, 8
 
 _lib = None
 
@@ -71,6 +72,10 @@ def lib():
             "kr_q4_mlp_workspace_bytes": (sz, [u32, u32, u32]),
             "kr_q4_qkv": (i32, [M, M, M, vp, vp, vp, vp, u32, vp, vp, vp, i32, vp]),
             "kr_q4_mlp": (i32, [M, M, M, vp, vp, i32, u32, i32, vp, sz, vp]),
+            "kr_moe_route": (i32, [vp, u32, u32, u32, i32, vp, vp, vp, vp, vp, vp]),
+            "kr_moe_scan_scatter": (i32, [vp, u32, u32, vp, vp, vp, vp]),
+            "kr_q4_moe_workspace_bytes": (sz, [u32, u32, u32, u32]),
+            "kr_q4_moe_experts": (i32, [M, M, M, u32, vp, u32, u32, vp, vp, vp, i32, vp, i32, i32, vp, sz, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -228,6 +233,65 @@ def mlp(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, h: torch.Tensor, x: Option
     _check(lib().kr_q4_mlp(gate.desc, up.desc, down.desc, _ptr(x), _ptr(h), _dt_of(h), m, activation,
                            _ptr(workspace), workspace.numel(), _stream(stream)))
     return h
+
+
+class MoeRoute:
+    """Device routing of one MoE step (kr_moe_route outputs)."""
+
+    def __init__(self, tokens: int, experts: int, topk: int, device="cuda"):
+        self.tokens, self.experts, self.topk = tokens, experts, topk
+        self.selected = torch.empty((tokens, topk), dtype=torch.int32, device=device)
+        self.weights = torch.empty((tokens, topk), dtype=torch.float32, device=device)
+        self.counts = torch.empty(experts, dtype=torch.int32, device=device)
+        self.offsets = torch.empty(experts + 1, dtype=torch.int32, device=device)
+        self.sorted_assign = torch.empty(max(tokens * topk, 1), dtype=torch.int32, device=device)
+
+
+def moe_route(logits: torch.Tensor, topk: int, normalize: bool = True, out: Optional[MoeRoute] = None,
+              stream=None) -> MoeRoute:
+    """Softmax + top-k + deterministic scan/scatter of f32 logits [tokens, experts]."""
+    tokens, experts = logits.shape
+    if out is None:
+        out = MoeRoute(tokens, experts, topk, device=logits.device)
+    _check(lib().kr_moe_route(_ptr(logits), tokens, experts, topk, int(normalize), _ptr(out.selected),
+                              _ptr(out.weights), _ptr(out.counts), _ptr(out.offsets), _ptr(out.sorted_assign),
+                              _stream(stream)))
+    return out
+
+
+def moe_scan_scatter(selected: torch.Tensor, experts: int, stream=None):
+    """(counts, offsets, sorted_assign) of given int32 expert ids."""
+    n = selected.numel()
+    counts = torch.empty(experts, dtype=torch.int32, device=selected.device)
+    offsets = torch.empty(experts + 1, dtype=torch.int32, device=selected.device)
+    sorted_assign = torch.empty(max(n, 1), dtype=torch.int32, device=selected.device)
+    _check(lib().kr_moe_scan_scatter(_ptr(selected), n, experts, _ptr(counts), _ptr(offsets), _ptr(sorted_assign),
+                                     _stream(stream)))
+    return counts, offsets, sorted_assign[:n]
+
+
+def moe_workspace_bytes(tokens: int, topk: int, hidden: int, inter: int) -> int:
+    return int(lib().kr_q4_moe_workspace_bytes(tokens, topk, hidden, inter))
+
+
+def moe_workspace(tokens: int, topk: int, hidden: int, inter: int, device="cuda") -> torch.Tensor:
+    return torch.empty(max(moe_workspace_bytes(tokens, topk, hidden, inter), 16), dtype=torch.uint8, device=device)
+
+
+def moe_experts(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, experts: int, x: torch.Tensor, route: MoeRoute,
+                y: Optional[torch.Tensor] = None, out_dtype: int = DTYPE_F32, accumulate: bool = False,
+                activation: int = ACT_SWIGLU, workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """y[t] (+)= sum_k w[t,k] * down_e(act(gate_e x_t) * up_e x_t) over the routed experts."""
+    tokens = route.tokens
+    if y is None:
+        y = torch.zeros((tokens, gate.k), dtype=_out_dtype(out_dtype), device=x.device)
+    if workspace is None:
+        workspace = moe_workspace(tokens, route.topk, gate.k, gate.n // experts, device=x.device)
+    _check(lib().kr_q4_moe_experts(gate.desc, up.desc, down.desc, experts, _ptr(x), tokens, route.topk,
+                                   _ptr(route.weights), _ptr(route.offsets), _ptr(route.sorted_assign), activation,
+                                   _ptr(y), _dt_of(y), int(accumulate), _ptr(workspace), workspace.numel(),
+                                   _stream(stream)))
+    return y
 
 
 # ---- names of the reference operator surface (encoder.rs) -------------------------------

@@ -100,3 +100,30 @@ def test_format_argument_checks(kq):
     assert L.kr_f16_to_bf16(None, None, 0, None) == kq.KR_OK
     assert L.kr_f16_to_bf16(0x1001, 0x2000, 4, None) == kq.KR_E_ALIGN
     assert L.kr_q4_dequant(ctypes.byref(_mat(kq)), 0x1004, None) == kq.KR_E_ALIGN
+
+
+def test_moe_argument_checks(kq):
+    L = kq.lib()
+    p = 0x40000
+    # routing: topk in 1..min(E, 16), E <= 256, T * topk <= 16384
+    assert L.kr_moe_route(p, 4, 8, 0, 1, p, p, p, p, p, None) == kq.KR_E_INVALID
+    assert L.kr_moe_route(p, 4, 8, 9, 1, p, p, p, p, p, None) == kq.KR_E_INVALID
+    assert L.kr_moe_route(p, 4, 300, 4, 1, p, p, p, p, p, None) == kq.KR_E_INVALID
+    assert L.kr_moe_route(p, 4097, 60, 4, 1, p, p, p, p, p, None) == kq.KR_E_SHAPE
+    assert L.kr_moe_route(p + 2, 4, 8, 2, 1, p, p, p, p, p, None) == kq.KR_E_ALIGN
+    assert L.kr_moe_scan_scatter(p, 16385, 8, p, p, p, None) == kq.KR_E_SHAPE
+    assert L.kr_moe_scan_scatter(p, 4, 0, p, p, p, None) == kq.KR_E_INVALID
+    # experts: stacked shapes must agree
+    E, H, I = 4, 128, 64
+    g, u = _mat(kq, n=E * I, k=H), _mat(kq, n=E * I, k=H)
+    d = _mat(kq, n=E * H, k=I)
+    need = L.kr_q4_moe_workspace_bytes(2, 2, H, I)
+    assert need >= 4 * I * 2 + 4 * H * 4
+    args = (p, 2, 2, p, p, p, 0, p, kq.DTYPE_F32, 0, 0x80000, need, None)
+    assert L.kr_q4_moe_experts(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), 3, *args) == kq.KR_E_SHAPE
+    bad_d = _mat(kq, n=E * H, k=128)
+    assert L.kr_q4_moe_experts(ctypes.byref(g), ctypes.byref(u), ctypes.byref(bad_d), E, *args) == kq.KR_E_SHAPE
+    short = args[:-2] + (need - 16, None)
+    assert L.kr_q4_moe_experts(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), E, *short) == kq.KR_E_WORKSPACE
+    wide = _mat(kq, n=E * I, k=8192), _mat(kq, n=E * I, k=8192), _mat(kq, n=E * 8192, k=I)
+    assert L.kr_q4_moe_experts(*(ctypes.byref(w) for w in wide), E, *args) == kq.KR_E_UNSUPPORTED
