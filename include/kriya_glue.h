@@ -1,0 +1,51 @@
+/*
+ * kriya_glue.h — the non-Q4 steps of config 3's end-to-end decode, as a C ABI
+ * beside kriya_q4.h: RMSNorm, RoPE with KV-cache append, decode attention
+ * (GQA) and greedy argmax.  Conventions as in kriya_q4.h (device pointers,
+ * stream-ordered, 0 or a negative KR_E* code, message in kr_last_error()).
+ * These are simple, correct kernels; the Q4 matmuls carry the time.
+ */
+#ifndef KRIYA_GLUE_H
+#define KRIYA_GLUE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* rms_norm_bf16 (transformer_glue.metal:158-205):
+ * out[r, :] = bf16(x * rsqrt(mean(x^2) + eps) * w), x/out bf16 [rows, dim], w bf16 [dim].
+ * out may equal x. */
+int kr_rmsnorm(const uint16_t *x, const uint16_t *weight, uint32_t rows, uint32_t dim, float eps,
+               uint16_t *out, void *stream);
+
+/* fused_qknorm_rope_and_kv_append without q/k norm (paged_gqa_and_deltanet.metal:115-222),
+ * on a contiguous cache:
+ *   q   bf16 [batch, q_heads, head_dim], rotated in place;
+ *   k,v bf16 [batch, kv_heads, head_dim]; k rotated, both written to
+ *   k_cache/v_cache bf16 [batch, max_ctx, kv_heads, head_dim] at row positions[b].
+ * Rotation of pairs (d, d + head_dim/2): (x0 c - x1 s, x0 s + x1 c) with
+ * cos_sin f32 [max_ctx, head_dim/2, 2] (encoder.rs:1940-1950).  positions: device
+ * u32 [batch]; a position >= max_ctx leaves that sequence untouched. */
+int kr_rope_kv_append(uint16_t *q, const uint16_t *k, const uint16_t *v, const float *cos_sin,
+                      const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                      uint32_t head_dim, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx,
+                      void *stream);
+
+/* Decode attention: out[b, h] = softmax_p(q[b,h] . k[b,p,kvh] / sqrt(head_dim)) v[b,p,kvh]
+ * over p <= positions[b], kvh = h / (q_heads / kv_heads).  out bf16 [batch, q_heads, head_dim].
+ * Limits: q_heads % kv_heads == 0, head_dim <= 256 and even, max_ctx <= 8192. */
+int kr_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                        const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                        uint32_t head_dim, uint32_t max_ctx, uint16_t *out, void *stream);
+
+/* Greedy sampling (transformer_glue.metal:407-494, temperature 0):
+ * out[r] = index of the largest logits[r, :] (ties to the lowest index, NaN never taken). */
+int kr_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KRIYA_GLUE_H */

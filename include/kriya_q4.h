@@ -82,8 +82,6 @@ const char *kr_last_error(void);
 #define KR_OPT_GEMV_BLOCK_ROWS 4        /* rows per split-K block tile: 1, 2 (default), 4, 8 */
 #define KR_OPT_GEMV_PERSISTENT_BLOCKS 5 /* grid of the persistent wave kernel (1024)       */
 #define KR_OPT_SKINNY_MAX_BLOCKS 6      /* grid cap of the few-token kernel (512)          */
-#define KR_OPT_SKINNY_LANE_COLS 7       /* few-token kernel: columns per lane group, 64 or 128 (128) */
-#define KR_OPT_SKINNY_WAVES 8           /* few-token kernel: waves per block, 4 (default) or 8 */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 
@@ -200,13 +198,22 @@ int kr_moe_scan_scatter(const uint32_t *selected, uint32_t num_assign, uint32_t 
  * d_a to bf16; here they stay f32.
  * workspace: kr_q4_moe_workspace_bytes(tokens, topk, hidden, inter) bytes,
  * 16-byte aligned; calls sharing it must not overlap in time.
- * Limits: experts <= 256; hidden and inter <= 2048, or <= 4096 when a multiple of 128. */
+ * Limits: experts <= 256; hidden and inter multiples of 128 and <= 2048;
+ * scales and biases 4-byte aligned. */
 size_t kr_q4_moe_workspace_bytes(uint32_t tokens, uint32_t topk, uint32_t hidden, uint32_t inter);
 int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down,
                       uint32_t experts, const uint16_t *x, uint32_t tokens, uint32_t topk,
                       const float *weights, const uint32_t *offsets, const uint32_t *sorted_assign,
                       int activation, void *y, int y_dtype, int accumulate,
                       void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---- Q4 embedding lookup: transformer_glue.metal:122-152 (embedding_lookup_q4_g64),
+ *      dispatched at encoder.rs:4803-4846 ----
+ * out[t, :] = bf16(fma(q, s, b)) of row tokens[t] of w (the tied Q4 embedding
+ * [vocab, hidden]).  tokens: device u32 [count]; ids >= w->n give zero rows.
+ * out: bf16 [count, w->k], 2-byte aligned. */
+int kr_q4_embedding(const kr_q4_matrix *w, const uint32_t *tokens, uint32_t count, uint16_t *out,
+                    void *stream);
 
 #ifdef __cplusplus
 }

@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <string>
 
+#include "kriya_glue.h"
 #include "kriya_q4.h"
 #include "kr_internal.hpp"
 
@@ -150,8 +151,8 @@ hipError_t run_skinny(const Q4Mat &w, const Q4Mat *w2, const uint16_t *x, uint32
     return launch_splitk_reduce(r, w2 ? 2 : 1, s);
 }
 
-bool skinny_fits(uint32_t m, uint32_t k, bool have_partial) {
-    return m >= 2 && m <= kSkinnyMaxM && (have_partial || skinny_ksplit(k) == 1);
+bool skinny_fits(uint32_t m, const Q4Mat &w, bool have_partial) {
+    return m >= 2 && m <= kSkinnyMaxM && skinny_supported(w) && (have_partial || skinny_ksplit(w.k) == 1);
 }
 
 size_t partial_bytes(uint32_t m, uint32_t n, uint32_t k, int nw) {
@@ -216,14 +217,6 @@ int kr_set_option(int option, int value) {
             if (value < 1) return fail(KR_E_INVALID, "skinny max blocks must be >= 1");
             tuning().skinny_max_blocks = value;
             return ok();
-        case KR_OPT_SKINNY_LANE_COLS:
-            if (value != 64 && value != 128) return fail(KR_E_INVALID, "skinny lane columns must be 64 or 128");
-            tuning().skinny_lane_cols = value;
-            return ok();
-        case KR_OPT_SKINNY_WAVES:
-            if (value != 4 && value != 8) return fail(KR_E_INVALID, "skinny waves must be 4 or 8");
-            tuning().skinny_waves = value;
-            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -236,8 +229,6 @@ int kr_get_option(int option) {
         case KR_OPT_GEMV_BLOCK_ROWS: return tuning().gemv_block_rows;
         case KR_OPT_GEMV_PERSISTENT_BLOCKS: return tuning().gemv_persistent_blocks;
         case KR_OPT_SKINNY_MAX_BLOCKS: return tuning().skinny_max_blocks;
-        case KR_OPT_SKINNY_LANE_COLS: return tuning().skinny_lane_cols;
-        case KR_OPT_SKINNY_WAVES: return tuning().skinny_waves;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -290,7 +281,7 @@ int kr_q4_linear(const kr_q4_matrix *w, const uint16_t *x, uint32_t m, void *y, 
                                    : (y_dtype == KR_DTYPE_F32 ? kStoreF32 : kStoreBF16);
         return hip_status(launch_gemv(a, nullptr, x, y, epi, 0, nullptr, s), "kr_q4_linear");
     }
-    if (skinny_fits(m, w->k, false))
+    if (skinny_fits(m, to_mat(w), false))
         return hip_status(run_skinny(a, nullptr, x, m, y, nullptr, w->n, y_dtype, accumulate, 0, nullptr, s),
                           "kr_q4_linear");
     MfmaArgs args = mfma_args(x, m, w->k, y_dtype, accumulate);
@@ -317,7 +308,7 @@ int kr_q4_gate_up_act(const kr_q4_matrix *gate, const kr_q4_matrix *up, const ui
         const int epi = act_dtype == KR_DTYPE_F32 ? kGateUpF32 : kGateUpBF16;
         return hip_status(launch_gemv(g, &u, x, act_out, epi, activation, nullptr, s), "kr_q4_gate_up_act");
     }
-    if (skinny_fits(m, gate->k, false))
+    if (skinny_fits(m, to_mat(gate), false) && skinny_supported(to_mat(up)))
         return hip_status(run_skinny(g, &u, x, m, act_out, nullptr, gate->n, act_dtype, 0, activation, nullptr, s),
                           "kr_q4_gate_up_act");
     MfmaArgs args = mfma_args(x, m, gate->k, act_dtype, 0);
@@ -354,7 +345,7 @@ int kr_q4_qkv(const kr_q4_matrix *q, const kr_q4_matrix *k, const kr_q4_matrix *
         }
         return ok();
     }
-    if (skinny_fits(m, q->k, false)) {
+    if (skinny_fits(m, to_mat(q), false) && skinny_supported(to_mat(k)) && skinny_supported(to_mat(v))) {
         for (int i = 0; i < 3; ++i) {
             const hipError_t e = run_skinny(to_mat(mats[i]), nullptr, x, m, outs[i], biases[i], mats[i]->n, out_dtype,
                                             0, 0, nullptr, s);
@@ -402,7 +393,7 @@ int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matr
     if (m == 1) return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
     // down projection: few N tiles at small m, so K is split over blocks; partials live in the workspace
     float *partial = (float *)((char *)workspace + round_up((size_t)m * gate->n * 2, 256));
-    if (skinny_fits(m, down->k, true))
+    if (skinny_fits(m, to_mat(down), true))
         return hip_status(run_skinny(to_mat(down), nullptr, act, m, h, nullptr, down->n, h_dtype, 1, 0, partial,
                                      (hipStream_t)stream),
                           "kr_q4_mlp (down)");
@@ -468,7 +459,9 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
         return fail(KR_E_SHAPE, "down [%u,%u] does not stack %u experts of [%u,%u]", down->n, down->k, experts, hidden,
                     inter);
     if (!skinny_grouped_fits(hidden) || !skinny_grouped_fits(inter))
-        return fail(KR_E_UNSUPPORTED, "hidden=%u / inter=%u: rows longer than one block covers", hidden, inter);
+        return fail(KR_E_UNSUPPORTED, "hidden=%u / inter=%u: need multiples of 128 up to 2048", hidden, inter);
+    if (!skinny_supported(to_mat(gate)) || !skinny_supported(to_mat(up)) || !skinny_supported(to_mat(down)))
+        return fail(KR_E_ALIGN, "expert scales/biases must be 4-byte aligned");
     if (topk == 0 || topk > experts) return fail(KR_E_INVALID, "topk=%u must be in 1..experts", topk);
     if (!valid_dtype(y_dtype)) return fail(KR_E_INVALID, "y_dtype %d invalid", y_dtype);
     if (!valid_act(activation)) return fail(KR_E_INVALID, "activation %d invalid", activation);
@@ -524,6 +517,66 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
 
     return hip_status(launch_moe_combine(d, weights, tokens, topk, hidden, y, y_dtype == KR_DTYPE_F32, accumulate, s),
                       "kr_q4_moe_experts (combine)");
+}
+
+int kr_q4_embedding(const kr_q4_matrix *w, const uint32_t *tokens, uint32_t count, uint16_t *out, void *stream) {
+    if (int rc = check_matrix(w, "w")) return rc;
+    if (count == 0) return ok();
+    if (!tokens || !out) return fail(KR_E_INVALID, "tokens/out must be non-NULL");
+    if (!aligned(tokens, 4) || !aligned(out, 2)) return fail(KR_E_ALIGN, "tokens/out misaligned");
+    if (count > 65535) return fail(KR_E_SHAPE, "count=%u exceeds 65535", count);
+    return hip_status(launch_q4_embedding(to_mat(w), tokens, count, out, (hipStream_t)stream), "kr_q4_embedding");
+}
+
+int kr_rmsnorm(const uint16_t *x, const uint16_t *weight, uint32_t rows, uint32_t dim, float eps, uint16_t *out,
+               void *stream) {
+    if (rows == 0) return ok();
+    if (!x || !weight || !out) return fail(KR_E_INVALID, "NULL pointer");
+    if (dim == 0) return fail(KR_E_SHAPE, "dim must be positive");
+    if (!aligned(x, 2) || !aligned(weight, 2) || !aligned(out, 2)) return fail(KR_E_ALIGN, "bf16 arrays misaligned");
+    if (!(eps >= 0.0f)) return fail(KR_E_INVALID, "eps must be >= 0");
+    return hip_status(launch_rmsnorm(x, weight, rows, dim, eps, out, (hipStream_t)stream), "kr_rmsnorm");
+}
+
+static int check_heads(uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t max_ctx) {
+    if (q_heads == 0 || kv_heads == 0 || q_heads % kv_heads != 0)
+        return fail(KR_E_SHAPE, "q_heads=%u must be a positive multiple of kv_heads=%u", q_heads, kv_heads);
+    if (head_dim == 0 || head_dim % 2 != 0 || head_dim > kGlueMaxHeadDim)
+        return fail(KR_E_SHAPE, "head_dim=%u must be even and <= %u", head_dim, kGlueMaxHeadDim);
+    if (max_ctx == 0 || max_ctx > kGlueMaxCtx) return fail(KR_E_SHAPE, "max_ctx=%u must be in 1..%u", max_ctx, kGlueMaxCtx);
+    return KR_OK;
+}
+
+int kr_rope_kv_append(uint16_t *q, const uint16_t *k, const uint16_t *v, const float *cos_sin,
+                      const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                      uint32_t head_dim, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx, void *stream) {
+    if (int rc = check_heads(q_heads, kv_heads, head_dim, max_ctx)) return rc;
+    if (batch == 0) return ok();
+    if (!q || !k || !v || !cos_sin || !positions || !k_cache || !v_cache) return fail(KR_E_INVALID, "NULL pointer");
+    if (batch > 65535) return fail(KR_E_SHAPE, "batch=%u exceeds 65535", batch);
+    return hip_status(launch_rope_kv_append(q, k, v, cos_sin, positions, batch, q_heads, kv_heads, head_dim, k_cache,
+                                            v_cache, max_ctx, (hipStream_t)stream),
+                      "kr_rope_kv_append");
+}
+
+int kr_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                        const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                        uint32_t head_dim, uint32_t max_ctx, uint16_t *out, void *stream) {
+    if (int rc = check_heads(q_heads, kv_heads, head_dim, max_ctx)) return rc;
+    if (batch == 0) return ok();
+    if (!q || !k_cache || !v_cache || !positions || !out) return fail(KR_E_INVALID, "NULL pointer");
+    if (batch > 65535) return fail(KR_E_SHAPE, "batch=%u exceeds 65535", batch);
+    return hip_status(launch_attention_decode(q, k_cache, v_cache, positions, batch, q_heads, kv_heads, head_dim,
+                                              max_ctx, out, (hipStream_t)stream),
+                      "kr_attention_decode");
+}
+
+int kr_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, void *stream) {
+    if (rows == 0) return ok();
+    if (!logits || !out) return fail(KR_E_INVALID, "NULL pointer");
+    if (n == 0) return fail(KR_E_SHAPE, "n must be positive");
+    if (!aligned(logits, 4) || !aligned(out, 4)) return fail(KR_E_ALIGN, "logits/out misaligned");
+    return hip_status(launch_argmax(logits, rows, n, out, (hipStream_t)stream), "kr_argmax");
 }
 
 }  // extern "C"

@@ -30,8 +30,6 @@ struct Tuning {
     int gemv_split_k_chunks = 0;       // rows of >= this many 16-byte chunks use the block kernel
                                        // (always beyond 128 chunks); 0 = default
     int skinny_max_blocks = 512;       // grid cap of the few-token kernel (blocks walk runs of tiles)
-    int skinny_lane_cols = 128;        // few-token kernel: columns per lane group (64 or 128)
-    int skinny_waves = 4;              // few-token kernel: K ranges (waves) per block (4 or 8)
 };
 Tuning &tuning();
 
@@ -112,6 +110,22 @@ hipError_t launch_moe_combine(const float *d, const float *w, uint32_t T, uint32
 uint32_t skinny_ksplit(uint32_t k);
 // True when one block of the grouped kernel covers rows of k columns (no K split).
 bool skinny_grouped_fits(uint32_t k);
+// The few-token kernel needs k % 128 == 0 and 4-byte aligned scales/biases.
+bool skinny_supported(const Q4Mat &w);
+
+// ---- embedding and end-to-end glue (e2e_glue.hip)
+constexpr uint32_t kGlueMaxCtx = 8192;
+constexpr uint32_t kGlueMaxHeadDim = 256;
+hipError_t launch_q4_embedding(const Q4Mat &w, const uint32_t *tokens, uint32_t count, uint16_t *out, hipStream_t s);
+hipError_t launch_rmsnorm(const uint16_t *x, const uint16_t *weight, uint32_t rows, uint32_t dim, float eps,
+                          uint16_t *out, hipStream_t s);
+hipError_t launch_rope_kv_append(uint16_t *q, const uint16_t *k, const uint16_t *v, const float *cos_sin,
+                                 const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                                 uint32_t D, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx, hipStream_t s);
+hipError_t launch_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                                   const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                                   uint32_t D, uint32_t max_ctx, uint16_t *out, hipStream_t s);
+hipError_t launch_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, hipStream_t s);
 
 // y = W x for one token; `b` is the up matrix for the gate/up epilogues;
 // `bias` (bf16 [n] or nullptr) is added by the store epilogues.

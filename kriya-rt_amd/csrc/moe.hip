@@ -22,85 +22,115 @@
 
 namespace kr {
 
-// softmax over E logits, then top-K by insertion (q4_gemm_and_moe.metal:2509-2568).
-// K <= kRouteMaxTopK; the arrays are indexed with compile-time indices only so
-// that they stay in registers.
-__device__ __forceinline__ void route_token(const float *l, uint32_t E, uint32_t K, int normalize, uint32_t *ti,
-                                            float *tv) {
-    float mx = -INFINITY;
-    for (uint32_t e = 0; e < E; ++e) mx = fmaxf(mx, l[e]);
-    float sum = 0.0f;
-    for (uint32_t e = 0; e < E; ++e) sum += expf(l[e] - mx);
+// Softmax over E logits and top-K selection for one token, on one wave
+// (q4_gemm_and_moe.metal:2509-2568).  Lane l holds experts l + 64 i.  The
+// maximum and the softmax denominator are taken in increasing expert order, as
+// the reference's serial loops do, so every probability is the reference's
+// value.  The reference's insertion with strict '>' yields the K largest
+// probabilities in descending order, ties by increasing id, NaN never taken,
+// and (0, -inf) in slots left empty.  Here each expert's position in that
+// order is its rank: the number of experts with a larger probability, or an
+// equal one and a lower id (counted against the wave's probabilities in LDS);
+// rank < K is the slot.  `pr` is this wave's LDS scratch of kMaxExperts floats;
+// ti/tv receive the K slots.
+__device__ void route_token_wave(const float *l, uint32_t E, uint32_t K, int normalize, uint32_t lane, float *pr,
+                                 uint32_t *ti, float *tv) {
+    constexpr int kPer = (int)(kMaxExperts / 64);
+    float lv[kPer];
 #pragma unroll
-    for (uint32_t k = 0; k < kRouteMaxTopK; ++k) {
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t e = lane + 64u * i;
+        lv[i] = e < E ? l[e] : -INFINITY;
+    }
+    float mx = -INFINITY;
+    float ex[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        if (64u * i >= E) break;
+        const uint32_t n = min(64u, E - 64u * i);
+        for (uint32_t j = 0; j < n; ++j) mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv[i]), j)));
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) ex[i] = (lane + 64u * i) < E ? expf(lv[i] - mx) : 0.0f;
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        if (64u * i >= E) break;
+        const uint32_t n = min(64u, E - 64u * i);
+        for (uint32_t j = 0; j < n; ++j) sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex[i]), j));
+    }
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t e = lane + 64u * i;
+        if (e < E) pr[e] = ex[i] / sum;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint32_t valid = 0;  // experts with a non-NaN probability
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const uint32_t e = lane + 64u * i;
+        if (64u * i >= E) break;
+        const bool in = e < E;
+        const float p = in ? pr[e] : 0.0f;
+        valid += (uint32_t)__popcll(__ballot(in && p == p));
+        if (!in || p != p) continue;
+        uint32_t rank = 0;
+        for (uint32_t o = 0; o < E; ++o) {
+            const float q = pr[o];
+            rank += (q > p || (q == p && o < e)) ? 1u : 0u;
+        }
+        if (rank < K) {
+            ti[rank] = e;
+            tv[rank] = p;
+        }
+    }
+    for (uint32_t k = valid; k < K; ++k) {  // the reference leaves (0, -inf) in unfilled slots
         ti[k] = 0;
         tv[k] = -INFINITY;
     }
-    for (uint32_t e = 0; e < E; ++e) {
-        const float prob = expf(l[e] - mx) / sum;
-        float last = tv[0];
-#pragma unroll
-        for (uint32_t k = 1; k < kRouteMaxTopK; ++k)
-            if (k == K - 1) last = tv[k];
-        if (!(prob > last)) continue;
-#pragma unroll
-        for (uint32_t k = 0; k < kRouteMaxTopK; ++k)
-            if (k == K - 1) {
-                tv[k] = prob;
-                ti[k] = e;
-            }
-        // bubble the new entry up; the rest of the list is sorted descending,
-        // so comparisons past the insertion point never swap
-#pragma unroll
-        for (int j = (int)kRouteMaxTopK - 2; j >= 0; --j) {
-            if (j + 1 <= (int)K - 1 && tv[j + 1] > tv[j]) {
-                const float fv = tv[j];
-                tv[j] = tv[j + 1];
-                tv[j + 1] = fv;
-                const uint32_t iv = ti[j];
-                ti[j] = ti[j + 1];
-                ti[j + 1] = iv;
-            }
-        }
-    }
-    float norm = 1.0f;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (normalize) {
-        norm = 0.0f;
-#pragma unroll
-        for (uint32_t k = 0; k < kRouteMaxTopK; ++k)
-            if (k < K) norm += tv[k];
+        float norm = 0.0f;
+        for (uint32_t k = 0; k < K; ++k) norm += tv[k];
         norm = fmaxf(norm, 1e-8f);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < K) tv[lane] = tv[lane] / norm;
     }
-#pragma unroll
-    for (uint32_t k = 0; k < kRouteMaxTopK; ++k)
-        if (k < K) tv[k] = tv[k] / norm;
 }
 
-// One block.  logits != nullptr: route (writes experts, weights); else the
-// assignments `experts` are given.  Then counts, offsets and the sorted list.
+// One block.  logits != nullptr: route one token per wave (writes experts,
+// weights); else the assignments `experts` are given.  Then counts, offsets
+// and the sorted list.
 __global__ __launch_bounds__(1024) void moe_route_kernel(const float *logits, uint32_t T, uint32_t E, uint32_t K,
                                                          int normalize, uint32_t *experts, float *weights,
                                                          uint32_t *counts, uint32_t *offsets, uint32_t *sorted) {
     __shared__ uint32_t s_cnt[kMaxExperts];
     __shared__ uint32_t s_off[kMaxExperts + 1];
+    __shared__ uint32_t s_ti[16][kRouteMaxTopK];
+    __shared__ float s_tv[16][kRouteMaxTopK];
+    __shared__ float s_pr[16][kMaxExperts];
     __shared__ uint16_t s_exp[kRouteMaxAssign];  // expert of each assignment; 0xFFFF: id >= E
     const uint32_t tid = threadIdx.x, nthreads = blockDim.x;
+    const uint32_t lane = tid & 63, wave = tid >> 6, waves = nthreads >> 6;
     const uint32_t total = T * K;
     for (uint32_t e = tid; e < E; e += nthreads) s_cnt[e] = 0;
     __syncthreads();
     if (logits) {
-        for (uint32_t t = tid; t < T; t += nthreads) {
-            uint32_t ti[kRouteMaxTopK];
-            float tv[kRouteMaxTopK];
-            route_token(logits + (size_t)t * E, E, K, normalize, ti, tv);
-#pragma unroll
-            for (uint32_t k = 0; k < kRouteMaxTopK; ++k) {
-                if (k < K) {
-                    experts[t * K + k] = ti[k];
-                    weights[t * K + k] = tv[k];
-                    s_exp[t * K + k] = (uint16_t)ti[k];
-                    atomicAdd(&s_cnt[ti[k]], 1u);  // counts only: the order of the adds does not matter
-                }
+        for (uint32_t t = wave; t < T; t += waves) {
+            route_token_wave(logits + (size_t)t * E, E, K, normalize, lane, s_pr[wave], s_ti[wave], s_tv[wave]);
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (lane < K) {
+                const uint32_t e = s_ti[wave][lane];
+                experts[t * K + lane] = e;
+                weights[t * K + lane] = s_tv[wave][lane];
+                s_exp[t * K + lane] = (uint16_t)e;
+                atomicAdd(&s_cnt[e], 1u);  // counts only: the order of the adds does not matter
             }
         }
     } else {
@@ -112,13 +142,28 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *logits, ui
         }
     }
     __syncthreads();
-    if (tid == 0) {
-        uint32_t run = 0;
-        for (uint32_t e = 0; e < E; ++e) {
-            s_off[e] = run;
-            run += s_cnt[e];
+    if (wave == 0) {  // exclusive scan: lane l owns experts 4l .. 4l+3
+        uint32_t c[4], run = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t e = 4 * lane + j;
+            c[j] = e < E ? s_cnt[e] : 0u;
+            run += c[j];
         }
-        s_off[E] = run;
+        uint32_t incl = run;
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            const uint32_t o = __shfl_up(incl, m);
+            if (lane >= (uint32_t)m) incl += o;
+        }
+        uint32_t off = incl - run;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t e = 4 * lane + j;
+            if (e < E) s_off[e] = off;
+            off += c[j];
+        }
+        if (lane == 63) s_off[E] = incl;
     }
     __syncthreads();
     for (uint32_t e = tid; e <= E; e += nthreads) {
@@ -127,7 +172,6 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *logits, ui
     }
     // scatter: wave w walks experts w, w + waves, ... and, for each, the
     // assignments in increasing id, 64 at a time
-    const uint32_t lane = tid & 63, wave = tid >> 6, waves = nthreads >> 6;
     const uint64_t below = (1ull << lane) - 1ull;
     for (uint32_t e = wave; e < E; e += waves) {
         uint32_t run = s_off[e];

@@ -29,7 +29,6 @@ DTYPE_BF16, DTYPE_F32 = 0, 1
 ACT_SWIGLU, ACT_GEGLU, ACT_RELU = 0, 1, 2
 OPT_GEMV_ROWS_PER_WAVE, OPT_GEMV_MAX_BLOCKS, OPT_GEMV_SPLIT_K_CHUNKS = 1, 2, 3
 OPT_GEMV_BLOCK_ROWS, OPT_GEMV_PERSISTENT_BLOCKS, OPT_SKINNY_MAX_BLOCKS = 4, 5, 6
-OPT_SKINNY_LANE_COLS, OPT_SKINNY_WAVES = 7, 8
 
 _lib = None
 

@@ -114,16 +114,18 @@ def test_moe_argument_checks(kq):
     assert L.kr_moe_scan_scatter(p, 16385, 8, p, p, p, None) == kq.KR_E_SHAPE
     assert L.kr_moe_scan_scatter(p, 4, 0, p, p, p, None) == kq.KR_E_INVALID
     # experts: stacked shapes must agree
-    E, H, I = 4, 128, 64
+    E, H, I = 4, 128, 128
     g, u = _mat(kq, n=E * I, k=H), _mat(kq, n=E * I, k=H)
     d = _mat(kq, n=E * H, k=I)
     need = L.kr_q4_moe_workspace_bytes(2, 2, H, I)
     assert need >= 4 * I * 2 + 4 * H * 4
     args = (p, 2, 2, p, p, p, 0, p, kq.DTYPE_F32, 0, 0x80000, need, None)
     assert L.kr_q4_moe_experts(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), 3, *args) == kq.KR_E_SHAPE
-    bad_d = _mat(kq, n=E * H, k=128)
+    bad_d = _mat(kq, n=E * H, k=256)
     assert L.kr_q4_moe_experts(ctypes.byref(g), ctypes.byref(u), ctypes.byref(bad_d), E, *args) == kq.KR_E_SHAPE
     short = args[:-2] + (need - 16, None)
     assert L.kr_q4_moe_experts(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), E, *short) == kq.KR_E_WORKSPACE
     wide = _mat(kq, n=E * I, k=8192), _mat(kq, n=E * I, k=8192), _mat(kq, n=E * 8192, k=I)
     assert L.kr_q4_moe_experts(*(ctypes.byref(w) for w in wide), E, *args) == kq.KR_E_UNSUPPORTED
+    odd = _mat(kq, n=E * 192, k=H), _mat(kq, n=E * 192, k=H), _mat(kq, n=E * H, k=192)
+    assert L.kr_q4_moe_experts(*(ctypes.byref(w) for w in odd), E, *args) == kq.KR_E_UNSUPPORTED

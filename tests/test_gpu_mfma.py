@@ -41,7 +41,8 @@ def test_gemm_reference_fixture_64x64x128(kq):
     assert_bf16_rounded_close(host_bits(yb), want, rms(want), what="gemm fixture bf16")
 
 
-@pytest.mark.parametrize("m,n,k", [(2, 300, 128), (4, 2048, 2048), (16, 1000, 2048), (17, 64, 64), (33, 130, 192),
+@pytest.mark.parametrize("m,n,k", [(2, 300, 128), (4, 2048, 2048), (16, 1000, 2048), (3, 200, 192), (7, 96, 512),
+                                   (9, 40, 1408), (17, 64, 64), (33, 130, 192),
                                    (64, 256, 1408), (100, 384, 512), (129, 96, 2048 + 64)])
 def test_linear_batched_shapes(kq, m, n, k):
     s = synth()

@@ -131,7 +131,8 @@ def moe_case(kq, T, E, K, hidden, inter, seed, logits=None):
     return (g, u, d, x, logits, route, want)
 
 
-@pytest.mark.parametrize("T,E,K,hidden,inter", [(8, 8, 4, 128, 64), (5, 6, 2, 256, 192), (1, 16, 4, 512, 1408)])
+@pytest.mark.parametrize("T,E,K,hidden,inter", [(8, 8, 4, 128, 128), (5, 6, 2, 256, 384), (1, 16, 4, 512, 1408),
+                                                (3, 5, 3, 1024, 256)])
 def test_moe_experts_small(kq, T, E, K, hidden, inter):
     case(f"moe experts T={T} E={E} K={K} hidden={hidden} inter={inter}")
     g, u, d, x, logits, route, want = moe_case(kq, T, E, K, hidden, inter, 4100 + T + E)
