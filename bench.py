@@ -116,11 +116,10 @@ def bench_mlp(kq, torch, synth, B, copies, steps, warmup):
         kq.q4_linear(d, act, y=h, accumulate=True)
 
     t_gu = graph_time_per_step(torch, gate_up, nsteps, replays, warm)
-    t_dn = graph_time_per_step(torch, down, nsteps, replays, warm)
-    out["kernels"] = {
-        "gate_up_act": {"s": t_gu, "alg_bytes": 2 * Q4_BYTES(I, H) + 2 * B * H + 2 * B * I},
-        "down_acc": {"s": t_dn, "alg_bytes": Q4_BYTES(H, I) + 2 * B * I + 4 * B * H},
-    }
+    out["kernels"] = {"gate_up_act": {"s": t_gu, "alg_bytes": 2 * Q4_BYTES(I, H) + 2 * B * H + 2 * B * I}}
+    if B == 1:  # m = 1: the down projection is one launch of its own (the GEMV with accumulate)
+        t_dn = graph_time_per_step(torch, down, nsteps, replays, warm)
+        out["kernels"]["down_acc"] = {"s": t_dn, "alg_bytes": Q4_BYTES(H, I) + 2 * B * I + 4 * B * H}
     for k in out["kernels"].values():
         k["gbs"] = k["alg_bytes"] / k["s"] / 1e9
     return out
@@ -139,6 +138,84 @@ def bench_gemv_cfg0(kq, torch, synth, copies, steps, warmup):
     t = graph_time_per_step(torch, step, nsteps, max(1, steps // nsteps), max(1, warmup // nsteps))
     alg = Q4_BYTES(N, K) + 2 * K + 2 * N
     return {"s_per_step": t, "alg_bytes": alg, "gbs": alg / t / 1e9}
+
+
+def bench_prefill_cfg2(kq, torch, synth, copies, steps):
+    """Config 2: the seven projections of one layer at M = 512 (q/k/v fused, o, gate/up fused, down)."""
+    M, H, I, KV = 512, 2048, 11008, 256
+    shapes = [(H, H), (KV, H), (KV, H), (H, H), (I, H), (I, H), (H, I)]  # q k v o gate up down
+    planars = [synth.q4_weight(n, k, 2000 + i) for i, (n, k) in enumerate(shapes)]
+    rot = Rotation(kq, torch, planars, copies)
+    x = torch.from_numpy(synth.bf16_normal((M, H), 2100).view(np.int16)).cuda().view(torch.bfloat16)
+    xi = torch.from_numpy(synth.bf16_normal((M, I), 2101).view(np.int16)).cuda().view(torch.bfloat16)
+    qo = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    ko = torch.empty((M, KV), dtype=torch.bfloat16, device="cuda")
+    vo = torch.empty((M, KV), dtype=torch.bfloat16, device="cuda")
+    oo = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    act = torch.empty((M, I), dtype=torch.bfloat16, device="cuda")
+    do = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+
+    def layer(i):
+        q, k, v, o, g, u, d = rot.sets[i % len(rot)]
+        kq.qkv(q, k, v, x, out_dtype=kq.DTYPE_BF16, outs=(qo, ko, vo))
+        kq.q4_linear(o, x, y=oo)
+        kq.gate_up_act(g, u, x, out=act)
+        kq.q4_linear(d, xi, y=do)
+
+    t = graph_time_per_step(torch, layer, len(rot), max(1, steps // (8 * len(rot))), 1)
+    flops = sum(2 * M * n * k for n, k in shapes)
+    tflops = flops / t / 1e12
+    return {"us": round(t * 1e6, 2), "tflops": round(tflops, 1), "mfma_util": round(tflops / MFMA_PEAK_TFLOPS, 4),
+            "flops_per_layer": flops, "m": M}
+
+
+def bench_decode_cfg3(torch, B, steps):
+    """Config 3: one greedy decode step of the 36-layer model at context 512, batch B."""
+    from kriya_q4.qwen_decode import QWEN25_3B, QwenQ4Decoder
+    m = QwenQ4Decoder(QWEN25_3B, batch=B, ctx=512, seed=3000 + B)
+    nsteps = 4
+    t = graph_time_per_step(torch, lambda i: m.step(), nsteps, max(1, steps // nsteps), 1)
+    bytes_step = QWEN25_3B.q4_bytes_per_step() + B * 36 * 513 * 2 * 256 * 2  # weights + KV read
+    out = {"B": B, "step_us": round(t * 1e6, 1), "tok_s": round(B / t, 1),
+           "gbs": round(bytes_step / t / 1e9, 1), "frac_hbm": round(bytes_step / t / 1e9 / HBM_PEAK_GBS, 4)}
+    del m
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_moe_cfg4(kq, torch, synth, copies, steps):
+    """Config 4: one MoE layer (60 experts, top-4, hidden 2048, inter 1408) at T = 1 and T = 64."""
+    E, K, H, I = 60, 4, 2048, 1408
+    planars = [synth.q4_weight(E * I, H, 4001), synth.q4_weight(E * I, H, 4002), synth.q4_weight(E * H, I, 4003)]
+    rot = Rotation(kq, torch, planars, copies)
+    res = {}
+    for T in (1, 64):
+        x = torch.from_numpy(synth.bf16_normal((T, H), 4004).view(np.int16)).cuda().view(torch.bfloat16)
+        logits = torch.from_numpy(synth.f32_normal((T, E), 4005)).cuda()
+        r = kq.MoeRoute(T, E, K)
+        ws = kq.moe_workspace(T, K, H, I)
+        y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+        kq.moe_route(logits, K, True, out=r)
+        torch.cuda.synchronize()
+        active = int((r.counts > 0).sum().item())
+
+        def step(i):
+            g, u, d = rot.sets[i % len(rot)]
+            kq.moe_route(logits, K, True, out=r)
+            kq.moe_experts(g, u, d, E, x, r, y=y, workspace=ws)
+
+        def experts(i):
+            g, u, d = rot.sets[i % len(rot)]
+            kq.moe_experts(g, u, d, E, x, r, y=y, workspace=ws)
+
+        t = graph_time_per_step(torch, step, len(rot), max(1, steps // (4 * len(rot))), 1)
+        te = graph_time_per_step(torch, experts, len(rot), max(1, steps // (4 * len(rot))), 1)
+        wbytes = active * 3 * Q4_BYTES(I, H)
+        res[f"T{T}"] = {"active_experts": active, "step_us": round(t * 1e6, 2), "experts_us": round(te * 1e6, 2),
+                        "tok_s": round(T / t, 1), "experts_gbs": round(wbytes / te / 1e9, 1),
+                        "experts_frac_hbm": round(wbytes / te / 1e9 / HBM_PEAK_GBS, 4),
+                        "tflops": round(2 * T * K * 3 * I * H / te / 1e12, 2)}
+    return res
 
 
 def cpu_baseline_mlp(synth, B, budget_s=12.0):
@@ -227,10 +304,19 @@ def main():
         for B in (4, 16):
             log(f"cfg1 B={B}")
             r = bench_mlp(kq, torch, synth, B, args.copies, args.steps, args.warmup)
+            gu = r["kernels"]["gate_up_act"]["s"]
             extra[f"cfg1_B{B}"] = {"step_us": round(r["s_per_step"] * 1e6, 3), "gbs": round(r["gbs"], 1),
                                    "frac_hbm": round(r["gbs"] / HBM_PEAK_GBS, 4),
                                    "tok_s": round(B / r["s_per_step"], 1),
-                                   "kernels_us": {k: round(v["s"] * 1e6, 3) for k, v in r["kernels"].items()}}
+                                   "kernels_us": {"gate_up_act": round(gu * 1e6, 3),
+                                                  "down_acc (step - gate_up)": round((r["s_per_step"] - gu) * 1e6, 3)}}
+        log("cfg2 prefill M=512")
+        extra["cfg2_prefill_M512"] = bench_prefill_cfg2(kq, torch, synth, 8, args.steps)
+        log("cfg4 MoE")
+        extra["cfg4_moe"] = bench_moe_cfg4(kq, torch, synth, 4, args.steps)
+        for B in (1, 16):
+            log(f"cfg3 decode B={B}")
+            extra[f"cfg3_decode_B{B}"] = bench_decode_cfg3(torch, B, min(args.steps, 200))
     result["extra"] = extra
     if not args.no_cpu:
         log("cpu baseline (oracle, cfg1 B=1)")

@@ -24,32 +24,35 @@ namespace kr {
 
 // Softmax over E logits and top-K selection for one token, on one wave
 // (q4_gemm_and_moe.metal:2509-2568).  Lane l holds experts l + 64 i.  The
-// maximum and the softmax denominator are taken in increasing expert order, as
-// the reference's serial loops do, so every probability is the reference's
-// value.  The reference's insertion with strict '>' yields the K largest
+// softmax denominator is summed in increasing expert order, as the reference's
+// serial loop does (the maximum does not depend on the order), so every
+// probability is the reference's value.  The reference's insertion with strict '>' yields the K largest
 // probabilities in descending order, ties by increasing id, NaN never taken,
 // and (0, -inf) in slots left empty.  Here each expert's position in that
 // order is its rank: the number of experts with a larger probability, or an
 // equal one and a lower id (counted against the wave's probabilities in LDS);
 // rank < K is the slot.  `pr` is this wave's LDS scratch of kMaxExperts floats;
 // ti/tv receive the K slots.
-__device__ void route_token_wave(const float *l, uint32_t E, uint32_t K, int normalize, uint32_t lane, float *pr,
-                                 uint32_t *ti, float *tv) {
-    constexpr int kPer = (int)(kMaxExperts / 64);
-    float lv[kPer];
+constexpr int kRoutePer = (int)(kMaxExperts / 64);  // logits per lane
+
+// This lane's logits of one token (experts lane + 64 i; -inf past E).
+__device__ __forceinline__ void load_logits(const float *l, uint32_t E, uint32_t lane, float (&lv)[kRoutePer]) {
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
+    for (int i = 0; i < kRoutePer; ++i) {
         const uint32_t e = lane + 64u * i;
         lv[i] = e < E ? l[e] : -INFINITY;
     }
-    float mx = -INFINITY;
-    float ex[kPer];
+}
+
+__device__ void route_token_wave(const float (&lv)[kRoutePer], uint32_t E, uint32_t K, int normalize, uint32_t lane,
+                                 float *pr, uint32_t *ti, float *tv) {
+    constexpr int kPer = kRoutePer;
+    float mx = -INFINITY;  // the maximum does not depend on the order
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        if (64u * i >= E) break;
-        const uint32_t n = min(64u, E - 64u * i);
-        for (uint32_t j = 0; j < n; ++j) mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lv[i]), j)));
-    }
+    for (int i = 0; i < kPer; ++i) mx = fmaxf(mx, lv[i]);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+    float ex[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) ex[i] = (lane + 64u * i) < E ? expf(lv[i] - mx) : 0.0f;
     float sum = 0.0f;
@@ -63,6 +66,7 @@ __device__ void route_token_wave(const float *l, uint32_t E, uint32_t K, int nor
     for (int i = 0; i < kPer; ++i) {
         const uint32_t e = lane + 64u * i;
         if (e < E) pr[e] = ex[i] / sum;
+        else if (e < ((E + 3) & ~3u)) pr[e] = __int_as_float(0x7FC00000);  // NaN pads the last float4
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -77,9 +81,15 @@ __device__ void route_token_wave(const float *l, uint32_t E, uint32_t K, int nor
         valid += (uint32_t)__popcll(__ballot(in && p == p));
         if (!in || p != p) continue;
         uint32_t rank = 0;
-        for (uint32_t o = 0; o < E; ++o) {
-            const float q = pr[o];
-            rank += (q > p || (q == p && o < e)) ? 1u : 0u;
+        const f32x4 *pr4 = reinterpret_cast<const f32x4 *>(pr);
+#pragma unroll 4
+        for (uint32_t o4 = 0; o4 < (E + 3) / 4; ++o4) {
+            const f32x4 q = pr4[o4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t o = 4 * o4 + c;
+                rank += (q[c] > p || (q[c] == p && o < e)) ? 1u : 0u;  // NaN pads never count
+            }
         }
         if (rank < K) {
             ti[rank] = e;
@@ -112,7 +122,7 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *logits, ui
     __shared__ uint32_t s_off[kMaxExperts + 1];
     __shared__ uint32_t s_ti[16][kRouteMaxTopK];
     __shared__ float s_tv[16][kRouteMaxTopK];
-    __shared__ float s_pr[16][kMaxExperts];
+    __shared__ __attribute__((aligned(16))) float s_pr[16][kMaxExperts];
     __shared__ uint16_t s_exp[kRouteMaxAssign];  // expert of each assignment; 0xFFFF: id >= E
     const uint32_t tid = threadIdx.x, nthreads = blockDim.x;
     const uint32_t lane = tid & 63, wave = tid >> 6, waves = nthreads >> 6;
@@ -120,8 +130,14 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *logits, ui
     for (uint32_t e = tid; e < E; e += nthreads) s_cnt[e] = 0;
     __syncthreads();
     if (logits) {
+        // the next token's logits are requested before the current token is routed
+        float lv[kRoutePer], ln[kRoutePer];
+        if (wave < T) load_logits(logits + (size_t)wave * E, E, lane, ln);
         for (uint32_t t = wave; t < T; t += waves) {
-            route_token_wave(logits + (size_t)t * E, E, K, normalize, lane, s_pr[wave], s_ti[wave], s_tv[wave]);
+#pragma unroll
+            for (int i = 0; i < kRoutePer; ++i) lv[i] = ln[i];
+            if (t + waves < T) load_logits(logits + (size_t)(t + waves) * E, E, lane, ln);
+            route_token_wave(lv, E, K, normalize, lane, s_pr[wave], s_ti[wave], s_tv[wave]);
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

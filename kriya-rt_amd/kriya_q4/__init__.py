@@ -75,6 +75,11 @@ def lib():
             "kr_moe_scan_scatter": (i32, [vp, u32, u32, vp, vp, vp, vp]),
             "kr_q4_moe_workspace_bytes": (sz, [u32, u32, u32, u32]),
             "kr_q4_moe_experts": (i32, [M, M, M, u32, vp, u32, u32, vp, vp, vp, i32, vp, i32, i32, vp, sz, vp]),
+            "kr_q4_embedding": (i32, [M, vp, u32, vp, vp]),
+            "kr_rmsnorm": (i32, [vp, vp, u32, u32, ctypes.c_float, vp, vp]),
+            "kr_rope_kv_append": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, u32, vp]),
+            "kr_attention_decode": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, vp]),
+            "kr_argmax": (i32, [vp, u32, u32, vp, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -291,6 +296,50 @@ def moe_experts(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, experts: int, x: t
                                    _ptr(y), _dt_of(y), int(accumulate), _ptr(workspace), workspace.numel(),
                                    _stream(stream)))
     return y
+
+
+def embedding(w: Q4Matrix, tokens: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """bf16 rows of the Q4 table for int32 token ids (transformer_glue.metal:122-152)."""
+    count = tokens.numel()
+    if out is None:
+        out = torch.empty((count, w.k), dtype=torch.bfloat16, device=tokens.device)
+    _check(lib().kr_q4_embedding(w.desc, _ptr(tokens), count, _ptr(out), _stream(stream)))
+    return out
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: Optional[torch.Tensor] = None,
+            stream=None) -> torch.Tensor:
+    dim = weight.numel()
+    rows = x.numel() // dim
+    if out is None:
+        out = torch.empty_like(x)
+    _check(lib().kr_rmsnorm(_ptr(x), _ptr(weight), rows, dim, eps, _ptr(out), _stream(stream)))
+    return out
+
+
+def rope_kv_append(q, k, v, cos_sin, positions, q_heads, kv_heads, head_dim, k_cache, v_cache, stream=None):
+    batch = positions.numel()
+    max_ctx = k_cache.shape[1]
+    _check(lib().kr_rope_kv_append(_ptr(q), _ptr(k), _ptr(v), _ptr(cos_sin), _ptr(positions), batch, q_heads,
+                                   kv_heads, head_dim, _ptr(k_cache), _ptr(v_cache), max_ctx, _stream(stream)))
+
+
+def attention_decode(q, k_cache, v_cache, positions, q_heads, kv_heads, head_dim, out=None, stream=None):
+    batch = positions.numel()
+    max_ctx = k_cache.shape[1]
+    if out is None:
+        out = torch.empty((batch, q_heads * head_dim), dtype=torch.bfloat16, device=q.device)
+    _check(lib().kr_attention_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(positions), batch, q_heads,
+                                     kv_heads, head_dim, max_ctx, _ptr(out), _stream(stream)))
+    return out
+
+
+def argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    rows, n = logits.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    _check(lib().kr_argmax(_ptr(logits), rows, n, _ptr(out), _stream(stream)))
+    return out
 
 
 # ---- names of the reference operator surface (encoder.rs) -------------------------------

@@ -1,0 +1,197 @@
+"""Config 3 (end-to-end decode) on the GPU: the Q4 embedding lookup bit-exact
+against the oracle's dequantisation, the glue kernels against numpy
+restatements of the reference's formulas, and one greedy decode step of a
+small Qwen2-shaped model against a layer-by-layer CPU restatement that uses
+the oracle's Q4 matmuls and rounds to bf16 where the device stores bf16.
+
+Bars: embedding bit-exact; glue within a few bf16 ulps; decode-step logits
+max |gpu - cpu| <= 3e-2 * RMS(cpu): the 1e-2 matmul bar per projection,
+compounded over the 2 x 7 projections and the bf16 roundings between them
+(one bf16 ulp is 2^-8 of a value), and the greedy token equal unless the
+CPU's top two logits are closer than that bound.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from _util import assert_rms_close, dev_bf16, host_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def bf(a):
+    """round f32 values to bf16 (RNE) and back"""
+    return O.bf16_to_f32(O.f32_to_bf16(np.asarray(a, np.float32)))
+
+
+def planar(m):
+    return O.Q4Planar(m.qw.cpu().numpy().view(np.uint32), m.scales.cpu().numpy().view(np.uint16),
+                      m.biases.cpu().numpy().view(np.uint16))
+
+
+def f32(t):
+    return t.float().cpu().numpy()
+
+
+def test_embedding_bit_exact(kq):
+    case("q4 embedding")
+    from kriya_q4 import synth
+    w = synth.q4_weight(300, 256, 3301)
+    tokens = np.array([0, 299, 17, 17, 150, 300], np.int32)  # 300 is out of range -> zero row
+    out = kq.embedding(kq.Q4Matrix.from_numpy(*w), torch.from_numpy(tokens).cuda())
+    deq = O.dequant_planar(O.Q4Planar(*w))
+    want = O.f32_to_bf16(deq[np.minimum(tokens, 299)])
+    want[-1] = 0
+    assert np.array_equal(host_bits(out), want)
+
+
+def test_rmsnorm(kq):
+    case("rmsnorm")
+    from kriya_q4 import synth
+    x = synth.bf16_normal((5, 320), 3302)
+    w = synth.bf16_normal((320,), 3303)
+    got = O.bf16_to_f32(host_bits(kq.rmsnorm(dev_bf16(x), dev_bf16(w), 1e-6)))
+    xf, wf = O.bf16_to_f32(x), O.bf16_to_f32(w)
+    scale = 1.0 / np.sqrt((xf.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    want = xf * scale * wf
+    assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-6)
+
+
+def rope_np(x, pos, cos_sin):
+    """pairs (d, d + D/2) rotated by the table row of `pos`"""
+    D = x.shape[-1]
+    h = D // 2
+    c, s = cos_sin[pos, :, 0], cos_sin[pos, :, 1]
+    x0, x1 = x[..., :h], x[..., h:]
+    return np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], axis=-1)
+
+
+def attention_np(q, kc, vc, pos, q_heads, kv_heads):
+    """q [H, D]; kc, vc [ctx, KVH, D]; positions 0..pos"""
+    D = q.shape[-1]
+    out = np.empty_like(q)
+    for h in range(q_heads):
+        kvh = h // (q_heads // kv_heads)
+        k = kc[: pos + 1, kvh].astype(np.float64)
+        v = vc[: pos + 1, kvh].astype(np.float64)
+        sc = k @ q[h].astype(np.float64) / math.sqrt(D)
+        p = np.exp(sc - sc.max())
+        out[h] = (p @ v) / p.sum()
+    return out
+
+
+def test_rope_append_and_attention(kq):
+    from kriya_q4 import synth
+    from kriya_q4.qwen_decode import rope_table
+    B, H, KVH, D, ctx = 3, 8, 2, 64, 12
+    case(f"rope + kv append + attention B={B} H={H}/{KVH} D={D} ctx={ctx}")
+    q = synth.bf16_normal((B, H * D), 3310)
+    k = synth.bf16_normal((B, KVH * D), 3311)
+    v = synth.bf16_normal((B, KVH * D), 3312)
+    kc = synth.bf16_normal((B, ctx, KVH, D), 3313)
+    vc = synth.bf16_normal((B, ctx, KVH, D), 3314)
+    pos = np.array([5, 11, 0], np.int32)
+    cs = rope_table(ctx, D, 1e6)
+    qd, kd, vd = dev_bf16(q), dev_bf16(k), dev_bf16(v)
+    kcd, vcd = dev_bf16(kc).clone(), dev_bf16(vc).clone()
+    posd = torch.from_numpy(pos).cuda()
+    kq.rope_kv_append(qd, kd, vd, cs.cuda(), posd, H, KVH, D, kcd, vcd)
+    att = kq.attention_decode(qd, kcd, vcd, posd, H, KVH, D)
+    csn = cs.numpy()
+    qf = O.bf16_to_f32(q).reshape(B, H, D)
+    kf = O.bf16_to_f32(k).reshape(B, KVH, D)
+    kc_want = O.bf16_to_f32(kc).copy()
+    vc_want = O.bf16_to_f32(vc).copy()
+    for b in range(B):
+        q_rot = bf(rope_np(qf[b], pos[b], csn))
+        assert np.all(np.abs(O.bf16_to_f32(host_bits(qd)).reshape(B, H, D)[b] - q_rot) <= np.abs(q_rot) * 2.0 ** -8 + 1e-6)
+        kc_want[b, pos[b]] = bf(rope_np(kf[b], pos[b], csn))
+        vc_want[b, pos[b]] = O.bf16_to_f32(v).reshape(B, KVH, D)[b]
+    got_kc = O.bf16_to_f32(host_bits(kcd))
+    assert np.all(np.abs(got_kc - kc_want) <= np.abs(kc_want) * 2.0 ** -8 + 1e-6)
+    assert np.array_equal(host_bits(vcd), O.f32_to_bf16(vc_want))
+    got = O.bf16_to_f32(host_bits(att)).reshape(B, H, D)
+    for b in range(B):
+        want = attention_np(O.bf16_to_f32(host_bits(qd)).reshape(B, H, D)[b], got_kc[b], vc_want[b], pos[b], H, KVH)
+        assert np.all(np.abs(got[b] - want) <= np.abs(want) * 2.0 ** -7 + 1e-3 * np.abs(want).max())
+
+
+def test_argmax_ties_and_nan(kq):
+    case("argmax")
+    x = np.random.default_rng(3).standard_normal((4, 1000)).astype(np.float32)
+    x[1, 10] = x[1, 700] = 50.0          # tie -> lowest index
+    x[2, :] = np.nan
+    x[2, 999] = -1.0                      # NaN never wins
+    x[3, 123] = np.inf
+    got = kq.argmax(torch.from_numpy(x).cuda()).cpu().numpy()
+    assert got.tolist() == [int(np.argmax(x[0])), 10, 999, 123]
+
+
+def decode_ref(m, cfg, tokens, pos):
+    """CPU restatement of one decode step (qwen_decode.QwenQ4Decoder.step)."""
+    B = len(tokens)
+    H, KVH, D = cfg.q_heads, cfg.kv_heads, cfg.head_dim
+    cs = m.cos_sin.cpu().numpy()
+    E = planar(m.embed)
+    h = bf(O.dequant_planar(E)[tokens])
+
+    def rms(v, w):
+        s = 1.0 / np.sqrt((v.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + cfg.eps)
+        return bf(v * s * f32(w))
+
+    def mm(W, v):
+        return O.q4_matmul(W, O.f32_to_bf16(v))
+
+    for L in m.layers:
+        x = rms(h, L.ln1)
+        q = bf(mm(planar(L.q), x) + f32(L.bq))
+        k = bf(mm(planar(L.k), x) + f32(L.bk))
+        v = bf(mm(planar(L.v), x) + f32(L.bv))
+        kc = f32(L.k_cache).copy()
+        vc = f32(L.v_cache).copy()
+        att = np.empty_like(q)
+        for b in range(B):
+            qb = bf(rope_np(q[b].reshape(H, D), pos[b], cs))
+            kc[b, pos[b]] = bf(rope_np(k[b].reshape(KVH, D), pos[b], cs))
+            vc[b, pos[b]] = v[b].reshape(KVH, D)
+            att[b] = bf(attention_np(qb, kc[b], vc[b], pos[b], H, KVH)).reshape(-1)
+        h = bf(h + mm(planar(L.o), att))
+        x = rms(h, L.ln2)
+        g = mm(planar(L.gate), x)
+        u = mm(planar(L.up), x)
+        a = bf(g / (1.0 + np.exp(-g)) * u)
+        h = bf(h + mm(planar(L.down), a))
+    x = rms(h, m.ln_f)
+    return mm(E, x)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_decode_step_small_model(kq, batch):
+    from kriya_q4.qwen_decode import QwenConfig, QwenQ4Decoder
+    cfg = QwenConfig(hidden=256, inter=512, layers=2, vocab=384, q_heads=4, kv_heads=2, head_dim=64)
+    case(f"decode step, small Qwen2-shaped model, batch={batch}")
+    m = QwenQ4Decoder(cfg, batch=batch, ctx=6, seed=3400 + batch)
+    tokens = m.tokens.cpu().numpy().copy()
+    pos = m.positions.cpu().numpy().copy()
+    caches0 = [(L.k_cache.clone(), L.v_cache.clone()) for L in m.layers]
+    nxt = m.step()
+    torch.cuda.synchronize()
+    logits = m.logits.cpu().numpy()
+    for L, (kc, vc) in zip(m.layers, caches0):  # the reference starts from the caches before the step
+        L.k_cache, L.v_cache = kc, vc
+    want = decode_ref(m, cfg, tokens, pos)
+    assert_rms_close(logits, want, rel=3e-2, what=f"decode logits B={batch}")
+    got_tok = nxt.cpu().numpy()
+    assert np.array_equal(got_tok, np.argmax(logits, axis=1))
+    bound = 3e-2 * np.sqrt((want.astype(np.float64) ** 2).mean())
+    for b in range(batch):
+        top2 = np.sort(want[b])[-2:]
+        if top2[1] - top2[0] > 2 * bound:
+            assert got_tok[b] == int(np.argmax(want[b]))
