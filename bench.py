@@ -243,6 +243,30 @@ def cpu_baseline_mlp(synth, B, budget_s=12.0):
                       f"C restatement (oracle/kr_oracle.c) on {threads} threads"}
 
 
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE runs scaled by a plain copy's counters), or None."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic_q4_gemv_cfg1_B1.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch="):
+                return int(line.split("=", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(torch):
+    """A plain device copy of known size (4 x 256 MiB) to scale the PMC byte counters."""
+    a = torch.empty(256 * 1024 * 1024 // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    log("copied 4 x 256 MiB")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -251,6 +275,8 @@ def main():
     ap.add_argument("--copies", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a 4 x 256 MiB device copy (PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
@@ -263,6 +289,9 @@ def main():
     from kriya_q4 import synth
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.calibrate_copy:
+        copy_calibration(torch)
+        return
     kq.lib()
     log(f"device {torch.cuda.get_device_name(0)}")
 
@@ -288,7 +317,9 @@ def main():
                    "launches_per_step": 2, "graph": "HIP graph replay"},
         "roofline": {"bound": "hbm", "kernel": "q4_gemv_wave_kernel<R,1,kGateUpBF16> (gate+up+silu fused, m=1)",
                      "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_source": "profiles/pmc_traffic_q4_gemv_cfg1_B1.md (rocprofv3 FETCH_SIZE/WRITE_SIZE, "
+                                       "copy-calibrated)",
                      "alg_bytes_per_launch": dom["alg_bytes"], "avg_launch_us": round(dom["s"] * 1e6, 3)},
         "cpu_baseline": None,
     }

@@ -28,7 +28,8 @@ int kr_rmsnorm(const uint16_t *x, const uint16_t *weight, uint32_t rows, uint32_
  *   k_cache/v_cache bf16 [batch, max_ctx, kv_heads, head_dim] at row positions[b].
  * Rotation of pairs (d, d + head_dim/2): (x0 c - x1 s, x0 s + x1 c) with
  * cos_sin f32 [max_ctx, head_dim/2, 2] (encoder.rs:1940-1950).  positions: device
- * u32 [batch]; a position >= max_ctx leaves that sequence untouched. */
+ * u32 [batch]; a position >= max_ctx leaves that sequence untouched.
+ * Limits: q_heads % kv_heads == 0, head_dim a multiple of 8 and <= 256, max_ctx <= 8192. */
 int kr_rope_kv_append(uint16_t *q, const uint16_t *k, const uint16_t *v, const float *cos_sin,
                       const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
                       uint32_t head_dim, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx,
@@ -36,7 +37,8 @@ int kr_rope_kv_append(uint16_t *q, const uint16_t *k, const uint16_t *v, const f
 
 /* Decode attention: out[b, h] = softmax_p(q[b,h] . k[b,p,kvh] / sqrt(head_dim)) v[b,p,kvh]
  * over p <= positions[b], kvh = h / (q_heads / kv_heads).  out bf16 [batch, q_heads, head_dim].
- * Limits: q_heads % kv_heads == 0, head_dim <= 256 and even, max_ctx <= 8192. */
+ * Limits: q_heads % kv_heads == 0, head_dim <= 256 and a multiple of 8, max_ctx <= 8192;
+ * q, k_cache, v_cache 16-byte aligned. */
 int kr_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                         const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
                         uint32_t head_dim, uint32_t max_ctx, uint16_t *out, void *stream);

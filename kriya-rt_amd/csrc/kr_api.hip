@@ -541,8 +541,8 @@ int kr_rmsnorm(const uint16_t *x, const uint16_t *weight, uint32_t rows, uint32_
 static int check_heads(uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim, uint32_t max_ctx) {
     if (q_heads == 0 || kv_heads == 0 || q_heads % kv_heads != 0)
         return fail(KR_E_SHAPE, "q_heads=%u must be a positive multiple of kv_heads=%u", q_heads, kv_heads);
-    if (head_dim == 0 || head_dim % 2 != 0 || head_dim > kGlueMaxHeadDim)
-        return fail(KR_E_SHAPE, "head_dim=%u must be even and <= %u", head_dim, kGlueMaxHeadDim);
+    if (head_dim == 0 || head_dim % 8 != 0 || head_dim > kGlueMaxHeadDim)
+        return fail(KR_E_SHAPE, "head_dim=%u must be a multiple of 8 and <= %u", head_dim, kGlueMaxHeadDim);
     if (max_ctx == 0 || max_ctx > kGlueMaxCtx) return fail(KR_E_SHAPE, "max_ctx=%u must be in 1..%u", max_ctx, kGlueMaxCtx);
     return KR_OK;
 }
@@ -565,6 +565,8 @@ int kr_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16
     if (int rc = check_heads(q_heads, kv_heads, head_dim, max_ctx)) return rc;
     if (batch == 0) return ok();
     if (!q || !k_cache || !v_cache || !positions || !out) return fail(KR_E_INVALID, "NULL pointer");
+    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16))
+        return fail(KR_E_ALIGN, "q, k_cache and v_cache must be 16-byte aligned");
     if (batch > 65535) return fail(KR_E_SHAPE, "batch=%u exceeds 65535", batch);
     return hip_status(launch_attention_decode(q, k_cache, v_cache, positions, batch, q_heads, kv_heads, head_dim,
                                               max_ctx, out, (hipStream_t)stream),
