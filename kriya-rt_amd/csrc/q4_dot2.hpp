@@ -76,20 +76,22 @@ struct GemvOut {
 };
 
 template <int EPI>
-__device__ __forceinline__ void store_row(const GemvOut &o, uint32_t row, float v) {
+// `pre` is the row's bias (store epilogues) or its old output value
+// (accumulate epilogues), read by tile_prefetch when the tile's weights were
+// requested, so that the store does not wait for a read.
+__device__ __forceinline__ void store_row(const GemvOut &o, uint32_t row, float v, float pre) {
     void *out = o.out;
     if (EPI == kStoreF32 || EPI == kStoreBF16) {
-        if (o.bias) v += bf16_to_f32(o.bias[row]);
+        if (o.bias) v += pre;
     }
     if (EPI == kStoreF32) {
         reinterpret_cast<float *>(out)[row] = v;
     } else if (EPI == kStoreBF16) {
         reinterpret_cast<uint16_t *>(out)[row] = (uint16_t)f32_to_bf16(v);
     } else if (EPI == kAccF32) {
-        reinterpret_cast<float *>(out)[row] += v;
+        reinterpret_cast<float *>(out)[row] = pre + v;
     } else if (EPI == kAccBF16) {  // res = bf16(f32(res) + y), q4_gemm_and_moe.metal:1407-1420
-        uint16_t *o = reinterpret_cast<uint16_t *>(out);
-        o[row] = (uint16_t)f32_to_bf16(v + bf16_to_f32(o[row]));
+        reinterpret_cast<uint16_t *>(out)[row] = (uint16_t)f32_to_bf16(v + pre);
     } else if (EPI == kGateUpF32) {
         reinterpret_cast<float *>(out)[row] = v;
     } else {
@@ -119,8 +121,22 @@ __device__ __forceinline__ void tile_rows(const Q4Mat &A, const Q4Mat &B, uint32
     }
 }
 
+// The value store_row needs besides the dot product (bias or old output) of
+// the row this lane stores for tile t; 0 when none.
 template <int R, int EPI>
-__device__ __forceinline__ void tile_epilogue(float tot, int lane, uint32_t t, uint32_t nrows, const GemvOut &o) {
+__device__ __forceinline__ float tile_prefetch(int lane, uint32_t t, uint32_t nrows, const GemvOut &o) {
+    constexpr int kSeg = kWave / R;
+    const uint32_t row = t * R + (uint32_t)(lane / kSeg);
+    if ((lane % kSeg) != 0 || row >= nrows) return 0.0f;
+    if (EPI == kAccF32) return reinterpret_cast<const float *>(o.out)[row];
+    if (EPI == kAccBF16) return bf16_to_f32(reinterpret_cast<const uint16_t *>(o.out)[row]);
+    if ((EPI == kStoreF32 || EPI == kStoreBF16) && o.bias) return bf16_to_f32(o.bias[row]);
+    return 0.0f;
+}
+
+template <int R, int EPI>
+__device__ __forceinline__ void tile_epilogue(float tot, int lane, uint32_t t, uint32_t nrows, const GemvOut &o,
+                                              float pre) {
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
     constexpr int kSeg = kWave / R;
     const int slot = lane / kSeg;
@@ -128,11 +144,11 @@ __device__ __forceinline__ void tile_epilogue(float tot, int lane, uint32_t t, u
         const float up = __shfl_xor(tot, kSeg);
         if ((lane % kSeg) == 0 && (slot & 1) == 0) {
             const uint32_t ch = t * (R / 2) + (slot >> 1);
-            if (ch < nrows) store_row<EPI>(o, ch, activation(tot, o.act) * up);
+            if (ch < nrows) store_row<EPI>(o, ch, activation(tot, o.act) * up, 0.0f);
         }
     } else if ((lane % kSeg) == 0) {
         const uint32_t row = t * R + slot;
-        if (row < nrows) store_row<EPI>(o, row, tot);
+        if (row < nrows) store_row<EPI>(o, row, tot, pre);
     }
 }
 

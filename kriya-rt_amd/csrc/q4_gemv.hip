@@ -77,6 +77,7 @@ __global__ __launch_bounds__(256) void q4_gemv_wave_kernel(Q4Mat A, Q4Mat B, con
         }
     };
     fetch(t);
+    float pre = tile_prefetch<R, EPI>(lane, t, A.n, o);
     for (;;) {
         // consume the fetched tile into accumulators, then prefetch the next one
         float acc[R];
@@ -90,11 +91,16 @@ __global__ __launch_bounds__(256) void q4_gemv_wave_kernel(Q4Mat A, Q4Mat B, con
             }
         }
         const uint32_t tn = t + nwaves;
-        if (tn < tiles) fetch(tn);
+        float pre_n = 0.0f;
+        if (tn < tiles) {
+            fetch(tn);
+            pre_n = tile_prefetch<R, EPI>(lane, tn, A.n, o);
+        }
         const float tot = wave_reduce_rows<R>(acc, lane);
-        tile_epilogue<R, EPI>(tot, lane, t, A.n, o);
+        tile_epilogue<R, EPI>(tot, lane, t, A.n, o, pre);
         if (tn >= tiles) break;
         t = tn;
+        pre = pre_n;
     }
 }
 
@@ -141,6 +147,7 @@ __global__ __launch_bounds__(256) void q4_gemv_block_kernel(Q4Mat A, Q4Mat B, co
 #pragma unroll
     for (int i = 0; i < C; ++i) live[i] = (tid + 256u * i) < nchunks;
     fetch(t);  // weights first: they do not depend on x
+    float pre = wave == 0 ? tile_prefetch<R, EPI>(lane, t, A.n, o) : 0.0f;
     XChunk xc[C];
 #pragma unroll
     for (int i = 0; i < C; ++i)
@@ -158,18 +165,23 @@ __global__ __launch_bounds__(256) void q4_gemv_block_kernel(Q4Mat A, Q4Mat B, co
             }
         }
         const uint32_t tn = t + gridDim.x;
-        if (tn < tiles) fetch(tn);
+        float pre_n = 0.0f;
+        if (tn < tiles) {
+            fetch(tn);
+            if (wave == 0) pre_n = tile_prefetch<R, EPI>(lane, tn, A.n, o);
+        }
         float tot = wave_reduce_rows<R>(acc, lane);
         const int slot = lane / kSeg;
         if ((lane % kSeg) == 0) red[wave][slot] = tot;
         __syncthreads();
         if (wave == 0) {
             tot = ((red[0][slot] + red[1][slot]) + red[2][slot]) + red[3][slot];
-            tile_epilogue<R, EPI>(tot, lane, t, A.n, o);
+            tile_epilogue<R, EPI>(tot, lane, t, A.n, o, pre);
         }
         if (tn >= tiles) break;
         __syncthreads();  // red is rewritten by the next tile
         t = tn;
+        pre = pre_n;
     }
 }
 
