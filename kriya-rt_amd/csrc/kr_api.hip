@@ -166,8 +166,10 @@ size_t partial_bytes(uint32_t m, uint32_t n, uint32_t k, int nw) {
 // Split K over the blocks when the tile grid alone would leave CUs idle.
 void choose_split_k(MfmaArgs &a, int bm, float *partial) {
     const uint32_t groups = a.k / 64;
-    const uint32_t rows = (uint32_t)bm_rows(bm);
-    const uint32_t tiles = ((a.m + rows - 1) / rows) * ((a.p[0].w.n + bn_of(bm, false) - 1) / bn_of(bm, false));
+    const bool prefill = bm > 16 && tuning().prefill_kernel == 0 && prefill_supported(a);
+    const uint32_t rows = prefill ? prefill_block_m(a.p[0].w2.qw != nullptr) : (uint32_t)bm_rows(bm);
+    const uint32_t cols = prefill ? prefill_block_rows(a.p[0].w2.qw != nullptr) : (uint32_t)bn_of(bm, false);
+    const uint32_t tiles = ((a.m + rows - 1) / rows) * ((a.p[0].w.n + cols - 1) / cols);
     const uint32_t target = 2u * (uint32_t)device_cus();
     uint32_t split = 1;
     while (split < kMaxSplitK && tiles * split < target && groups / (split * 2) >= 8) split *= 2;
@@ -217,6 +219,10 @@ int kr_set_option(int option, int value) {
             if (value < 1) return fail(KR_E_INVALID, "skinny max blocks must be >= 1");
             tuning().skinny_max_blocks = value;
             return ok();
+        case KR_OPT_PREFILL_KERNEL:
+            if (value != 0 && value != 1) return fail(KR_E_INVALID, "prefill kernel must be 0 or 1");
+            tuning().prefill_kernel = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -229,6 +235,7 @@ int kr_get_option(int option) {
         case KR_OPT_GEMV_BLOCK_ROWS: return tuning().gemv_block_rows;
         case KR_OPT_GEMV_PERSISTENT_BLOCKS: return tuning().gemv_persistent_blocks;
         case KR_OPT_SKINNY_MAX_BLOCKS: return tuning().skinny_max_blocks;
+        case KR_OPT_PREFILL_KERNEL: return tuning().prefill_kernel;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }

@@ -30,6 +30,8 @@ struct Tuning {
     int gemv_split_k_chunks = 0;       // rows of >= this many 16-byte chunks use the block kernel
                                        // (always beyond 128 chunks); 0 = default
     int skinny_max_blocks = 512;       // grid cap of the few-token kernel (blocks walk runs of tiles)
+    int prefill_kernel = 0;            // m > 16: 0 = register-dequant prefill kernel,
+                                       // 1 = LDS-dequant tiled kernel
 };
 Tuning &tuning();
 
@@ -70,6 +72,11 @@ struct MfmaArgs {
 
 // bm: the M tile class (16, 64 or 128) chosen by the caller from m.
 hipError_t launch_mfma(MfmaArgs &a, int bm, hipStream_t s);
+// Prefill kernel (q4_prefill.hip): m > 16, k % 64 == 0, operands < 4 GiB.
+bool prefill_supported(const MfmaArgs &a);
+hipError_t launch_prefill(MfmaArgs &a, hipStream_t s);
+uint32_t prefill_block_m(bool gate_up);         // token rows per block
+uint32_t prefill_block_rows(bool gate_up);      // weight rows (per matrix) per block
 // Fixed-order sum of split-K partials [ksplit, m, nw * N] + the epilogue of p[0].
 hipError_t launch_splitk_reduce(const MfmaArgs &a, int nw, hipStream_t s);
 

@@ -50,12 +50,12 @@ __device__ __forceinline__ uint32_t opaque_v(uint32_t v) {
     return r;
 }
 
-// bf16 bits -> fp16 bits (round to nearest even; exact in fp16's normal range).
+// bf16 bits -> fp16 bits.  A bf16 value has 8 significant bits, so in fp16's
+// normal range the conversion is exact and the rounding mode does not matter:
+// one v_cvt_pkrtz_f16_f32 per pair.
 __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v) {
-    const _Float16 lo = (_Float16)__uint_as_float(v << 16);
-    const _Float16 hi = (_Float16)__uint_as_float(v & 0xFFFF0000u);
-    f16x2_t p = {lo, hi};
-    return __builtin_bit_cast(uint32_t, p);
+    return __builtin_bit_cast(uint32_t,
+                              __builtin_amdgcn_cvt_pkrtz(__uint_as_float(v << 16), __uint_as_float(v & 0xFFFF0000u)));
 }
 
 // 8 nibbles of one word -> 8 fp16 weights in element order (e0..e7) as 4 u32.
@@ -334,6 +334,7 @@ static hipError_t launch_shape(MfmaArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_mfma(MfmaArgs &a, int bm, hipStream_t s) {
+    if (bm > 16 && tuning().prefill_kernel == 0 && prefill_supported(a)) return launch_prefill(a, s);
     const bool gate_up = a.p[0].w2.qw != nullptr;
     if (gate_up) {
         if (bm <= 16) return launch_shape<32, 32, 2>(a, s);

@@ -1,0 +1,354 @@
+// q4_prefill.hip — prefill-sized (m > 16) Q4_G64 matmul on the gfx950 matrix cores.
+//
+// Replaces the reference's M >= 64 simdgroup kernels (kernels/metal/q4_gemm_and_moe.metal):
+//   q4_g64_batched_simdgroup_gemm_m64                     :2708-2851
+//   q4_g64_batched_simdgroup_qkv_gemm_m64                 :2853-3022
+//   q4_g64_batched_simdgroup_gate_up_swiglu_gemm_m64      :3024-3215
+// and the 1 < M < 64 prefill kernels (:2173-2486) for m > 16.
+//
+// Y[M, N] = X[M, K] . W[N, K]^T, X bf16, W planar Q4_G64, f32 accumulation on
+// v_mfma_f32_16x16x32_f16.  Operand numerics are those of the reference's M >= 64
+// kernels (half operands, q4_gemm_and_moe.metal:2722-2724, 2761-2764):
+//   * w = fma(q, s, b) rounded once to fp16 (s, b: bf16 -> fp16 RNE);
+//   * x: bf16 -> fp16 RNE, exact for |x| in [2^-14, 65504].
+//
+// Where the time goes at these shapes (M = 512, K = 2048 .. 11008): dequantising
+// a nibble costs ~2 VALU lane-ops, converting an X element ~1.5, and the matrix
+// cores need 2 * M_reuse FLOP per weight element to stay ahead of the VALU.  So:
+//   * each wave owns MF x 16 token rows by NF x 16 weight rows and dequantises
+//     its weight rows itself, straight from global memory into the MFMA B
+//     fragments (no LDS round trip for W, no barrier between dequant and use);
+//     one dequantised word feeds MF matrix instructions;
+//   * X is staged in LDS by direct-to-LDS buffer loads (no VGPRs held across
+//     the step), converted to fp16 in place once per block (double buffered,
+//     one 64-column quantisation group per step, one barrier per step) and
+//     shared by the WAVES waves of the block, which split the weight rows;
+//   * the k order inside each 8-column unit is the nibble-pair order of the
+//     dequantiser, (e0 e4 e1 e5 e2 e6 e3 e7), applied to X when it is staged,
+//     so neither side permutes in the inner loop (a dot product does not depend
+//     on the order of its terms);
+//   * LDS rows of 8 units are XOR-swizzled by row so that the 16-byte reads of
+//     16 rows x 4 units and the staging writes are bank-conflict free;
+//   * weights, scales and X are read through buffer resources with the block-
+//     and step-uniform part of every offset in an SGPR; every offset is kept in
+//     range on the host side of the check (tail rows are clamped, never stored).
+// Gate/up: a wave's fragments are FPM gate fragments followed by FPM up
+// fragments of the same rows, so act(g) * u is formed lane-locally.
+// Block ids are remapped so that the M tiles of one N tile run on one XCD and
+// share its L2; split-K (grid.y) writes f32 partials that
+// q4_mfma_splitk_reduce_kernel sums in split order.
+#include "kr_internal.hpp"
+
+
+namespace kr {
+
+namespace {
+
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint32_t opaque_v(uint32_t v) {
+    uint32_t r;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
+    return r;
+}
+
+__device__ __forceinline__ f16x2_t f16_pair(uint32_t bf16_bits) {
+    const _Float16 h = (_Float16)bf16_to_f32(bf16_bits);
+    return f16x2_t{h, h};
+}
+
+// LDS row swizzle of the X slice: 16 consecutive rows x one unit hit 16
+// distinct 16-byte slots modulo 256 bytes, and 8 consecutive rows distinct
+// slots modulo 128 bytes.
+__device__ __forceinline__ uint32_t swz(uint32_t r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// 16 bytes per lane from a buffer straight into LDS: lane l writes lds[16 l, 16 l + 16).
+// `lds` must be wave-uniform (it goes to M0).
+__device__ __forceinline__ void dma16(rsrc_t r, char *lds, uint32_t voffset, uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds, 16, voffset, soffset, 0,
+                                             0);
+}
+
+// 8 nibbles of one word -> the B fragment (w0 w4)(w1 w5)(w2 w6)(w3 w7), w = fma(q, s, b).
+__device__ __forceinline__ f16x8_t dequant_pairs(uint32_t w, f16x2_t s2, f16x2_t b2, uint32_t mask, uint32_t magic) {
+    const f16x2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    f16x2_t pr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t h = ((w >> (4 * j)) & mask) | magic;           // (1024 + q_j, 1024 + q_{j+4})
+        pr[j] = __builtin_elementwise_fma(__builtin_bit_cast(f16x2_t, h) + k1024, s2, b2);
+    }
+    return f16x8_t{pr[0].x, pr[0].y, pr[1].x, pr[1].y, pr[2].x, pr[2].y, pr[3].x, pr[3].y};
+}
+
+// 8 bf16 columns (x0 x1)(x2 x3)(x4 x5)(x6 x7) -> fp16 (x0 x4)(x1 x5)(x2 x6)(x3 x7).
+__device__ __forceinline__ u32x4 x_unit_f16(u32x4 d) {
+    auto lo = [](uint32_t v) { return __uint_as_float(v << 16); };
+    auto hi = [](uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); };
+    const f16x2_t o0 = {(_Float16)lo(d.x), (_Float16)lo(d.z)};
+    const f16x2_t o1 = {(_Float16)hi(d.x), (_Float16)hi(d.z)};
+    const f16x2_t o2 = {(_Float16)lo(d.y), (_Float16)lo(d.w)};
+    const f16x2_t o3 = {(_Float16)hi(d.y), (_Float16)hi(d.w)};
+    return u32x4{__builtin_bit_cast(uint32_t, o0), __builtin_bit_cast(uint32_t, o1),
+                 __builtin_bit_cast(uint32_t, o2), __builtin_bit_cast(uint32_t, o3)};
+}
+
+}  // namespace
+
+template <int MF, int NF, int WAVES, int NW>
+struct PrefillTile {
+    static constexpr int kBM = MF * 16;                 // token rows per block
+    static constexpr int kThreads = 64 * WAVES;
+    static constexpr int kFPM = NF / NW;                // fragments per matrix per wave
+    static constexpr int kWaveRows = kFPM * 16;         // output columns per wave
+    static constexpr int kBN = WAVES * kWaveRows;       // output columns per block
+    static constexpr int kBufBytes = kBM * 128;         // one 64-column X slice in fp16
+    static constexpr int kLdsBytes = 2 * kBufBytes;
+    static_assert(NF % NW == 0, "gate/up needs pairs of fragments");
+};
+
+template <int MF, int NF, int WAVES, int NW, int OCC, int EPI>
+__global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs args) {
+    using T = PrefillTile<MF, NF, WAVES, NW>;
+    constexpr int FPM = T::kFPM;
+    extern __shared__ __align__(16) char lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 15, kq = lane >> 4;
+
+    // ---- block -> (problem, n tile, m tile); the M tiles of one N tile share an XCD
+    const uint32_t nblk = gridDim.x;
+    uint32_t bid = blockIdx.x;
+    if (nblk >= 8 && (nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxMfmaProblems; ++i)
+        if (i < args.np && bid >= args.p[i].tile_begin) pi = i;
+    const MfmaProblem &P = args.p[pi];
+    const uint32_t local = bid - P.tile_begin;
+    const uint32_t tiles_m = (args.m + T::kBM - 1) / T::kBM;
+    const uint32_t mt = local % tiles_m, nt = local / tiles_m;
+    const uint32_t m0 = mt * T::kBM;
+    const uint32_t N = P.w.n, M = args.m, K = args.k, G = K >> 6;
+    const uint32_t row0 = nt * T::kBN + wave * T::kWaveRows;  // first weight row of this wave
+    const uint32_t ks = blockIdx.y;
+    const uint32_t g_begin = ks * args.groups_per_split;
+    const uint32_t g_end = min(G, g_begin + args.groups_per_split);
+
+    const uint32_t kMask = opaque_v(0x000F000Fu);
+    const uint32_t kMagic = opaque_v(0x64006400u);
+
+    // ---- buffer resources and per-lane offsets (the step-uniform part goes in soffset)
+    const uint32_t rowbytes = K >> 1;
+    rsrc_t rq[NW], rs[NW], rb[NW];
+    rq[0] = make_rsrc(P.w.qw, N * rowbytes);
+    rs[0] = make_rsrc(P.w.sc, N * G * 2);
+    rb[0] = make_rsrc(P.w.bi, N * G * 2);
+    if constexpr (NW == 2) {
+        rq[1] = make_rsrc(P.w2.qw, N * rowbytes);
+        rs[1] = make_rsrc(P.w2.sc, N * G * 2);
+        rb[1] = make_rsrc(P.w2.bi, N * G * 2);
+    }
+    uint32_t oq[FPM], os[FPM];
+#pragma unroll
+    for (int f = 0; f < FPM; ++f) {
+        const uint32_t row = min(row0 + f * 16 + c, N - 1);  // tail rows re-read row N-1; never stored
+        oq[f] = row * rowbytes + kq * 8;
+        os[f] = row * G * 2;
+    }
+    // ---- X staging: direct-to-LDS loads (no VGPR round trip), converted in place.
+    // A buffer holds the block's BM rows x 8 units (16 B) of one 64-column slice;
+    // row r, unit u lives in slot r * 8 + (u ^ swz(r)).  DMA instruction i of a
+    // wave writes 64 consecutive slots (lane l -> slot base + l), so each lane
+    // loads the global unit that belongs in its slot and later converts exactly
+    // the slots it loaded (its own data: no barrier between load and convert).
+    constexpr int XI = T::kBM * 8 / 64 / WAVES;  // DMA instructions per wave per step
+    static_assert(T::kBM * 8 % (64 * WAVES) == 0, "X slice must split into whole DMA instructions");
+    const rsrc_t rx = make_rsrc(args.x, (M - 1) * args.ldx * 2 + K * 2);
+    uint32_t xo[XI];
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+        const uint32_t slot = (wave * XI + i) * 64 + lane;
+        const uint32_t r = slot >> 3, u = (slot & 7) ^ swz(r);
+        xo[i] = min(m0 + r, M - 1) * args.ldx * 2 + u * 16;  // tail rows re-read row M-1; never stored
+    }
+    auto dma_x = [&](uint32_t g, int buf) {
+#pragma unroll
+        for (int i = 0; i < XI; ++i) dma16(rx, lds + buf * T::kBufBytes + (wave * XI + i) * 1024, xo[i], g * 128);
+    };
+    auto convert_x = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            u32x4 *p = reinterpret_cast<u32x4 *>(lds + buf * T::kBufBytes + (wave * XI + i) * 1024 + lane * 16);
+            *p = x_unit_f16(*p);
+        }
+    };
+    // A fragment reads: row r = 16 * a + c (swz depends on c only), unit 2 * kq + j
+    const uint32_t xa0 = ((c * 8) + ((2 * kq + 0) ^ swz(c))) * 16;
+    const uint32_t xa1 = ((c * 8) + ((2 * kq + 1) ^ swz(c))) * 16;
+
+    struct WRegs {
+        u32x2 q[NF];
+        uint32_t s[NF], b[NF];
+    };
+    auto load_w = [&](uint32_t g, WRegs &r) {
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const int mi = f / FPM, fi = f % FPM;
+            r.q[f] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rq[mi], oq[fi], g * 32, 0));
+            r.s[f] = __builtin_amdgcn_raw_buffer_load_b16(rs[mi], os[fi], g * 2, 0);
+            r.b[f] = __builtin_amdgcn_raw_buffer_load_b16(rb[mi], os[fi], g * 2, 0);
+        }
+    };
+
+    f32x4 acc[MF][NF];
+#pragma unroll
+    for (int a = 0; a < MF; ++a)
+#pragma unroll
+        for (int f = 0; f < NF; ++f) acc[a][f] = f32x4{0, 0, 0, 0};
+
+    auto compute = [&](int buf, WRegs &w) {
+        f16x2_t s2[NF], b2[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            s2[f] = f16_pair(w.s[f]);
+            b2[f] = f16_pair(w.b[f]);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            f16x8_t bf[NF];
+#pragma unroll
+            for (int f = 0; f < NF; ++f) bf[f] = dequant_pairs(j == 0 ? w.q[f].x : w.q[f].y, s2[f], b2[f], kMask, kMagic);
+            const char *ab = lds + buf * T::kBufBytes + (j == 0 ? xa0 : xa1);
+#pragma unroll
+            for (int a = 0; a < MF; ++a) {
+                const f16x8_t af = *reinterpret_cast<const f16x8_t *>(ab + a * 2048);
+#pragma unroll
+                for (int f = 0; f < NF; ++f)
+                    acc[a][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[f], acc[a][f], 0, 0, 0);
+            }
+        }
+    };
+
+    if (g_begin < g_end) {
+        WRegs w0, w1;
+        dma_x(g_begin, 0);
+        load_w(g_begin, w0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        convert_x(0);
+        __syncthreads();
+        // Loads of the next step are issued unconditionally (the group index is
+        // clamped, so offsets stay inside the buffers): no branch sits between
+        // a load and its use.  X of step g+1 lands in the other buffer while
+        // step g computes; vmcnt counts in issue order, so waiting until only
+        // the weight loads issued after it are outstanding covers the DMA.
+        uint32_t g = g_begin;
+        int buf = 0;
+        constexpr int kWLoads = 3 * NF;
+        auto step = [&](uint32_t gn, WRegs &cur, WRegs &next) {
+            dma_x(gn, buf ^ 1);
+            __builtin_amdgcn_sched_barrier(0);  // the DMA is issued before the weight loads (vmcnt order)
+            load_w(gn, next);
+            __builtin_amdgcn_sched_barrier(0);  // keep the loads at the top of the step
+            compute(buf, cur);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kWLoads) : "memory");
+            convert_x(buf ^ 1);
+            __syncthreads();
+            buf ^= 1;
+        };
+        for (; g + 2 <= g_end; g += 2) {
+            step(min(g + 1, G - 1), w0, w1);
+            step(min(g + 2, G - 1), w1, w0);
+        }
+        if (g < g_end) compute(buf, w0);
+    }
+
+    // ---- epilogue: lane holds C[4 * kq + v][c] of each 16 x 16 fragment
+#pragma unroll
+    for (int fo = 0; fo < FPM; ++fo) {
+        const uint32_t n = row0 + fo * 16 + c;
+        if (n >= N) continue;
+        const float bias = (EPI == kMfmaDirect && P.bias) ? bf16_to_f32(P.bias[n]) : 0.0f;
+#pragma unroll
+        for (int a = 0; a < MF; ++a) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t m = m0 + a * 16 + 4 * kq + v;
+                if (m >= M) continue;
+                if (EPI == kMfmaPartial) {
+                    float *dst = args.partial + ((size_t)ks * M + m) * (size_t)(NW * N) + n;
+                    dst[0] = acc[a][fo][v];
+                    if (NW == 2) dst[N] = acc[a][fo + FPM][v];
+                    continue;
+                }
+                float val = acc[a][fo][v];
+                if (NW == 2) val = activation(val, args.act) * acc[a][fo + FPM][v];
+                val += bias;
+                const size_t o = (size_t)m * P.ldo + n;
+                if (args.out_f32) {
+                    float *out = reinterpret_cast<float *>(P.out);
+                    out[o] = args.accumulate ? out[o] + val : val;
+                } else {
+                    uint16_t *out = reinterpret_cast<uint16_t *>(P.out);
+                    out[o] = (uint16_t)f32_to_bf16(args.accumulate ? val + bf16_to_f32(out[o]) : val);
+                }
+            }
+        }
+    }
+}
+
+template <int MF, int NF, int WAVES, int NW, int OCC>
+static hipError_t launch_prefill_shape(MfmaArgs &a, hipStream_t s) {
+    using T = PrefillTile<MF, NF, WAVES, NW>;
+    uint32_t tiles = 0;
+    const uint32_t tiles_m = (a.m + T::kBM - 1) / T::kBM;
+    for (int i = 0; i < a.np; ++i) {
+        a.p[i].tile_begin = tiles;
+        tiles += tiles_m * ((a.p[i].w.n + T::kBN - 1) / T::kBN);
+    }
+    const dim3 grid(tiles, a.ksplit);
+    if (a.ksplit > 1) {
+        hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaPartial>), grid, dim3(T::kThreads),
+                           T::kLdsBytes, s, a);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_splitk_reduce(a, NW, s);
+    }
+    hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaDirect>), grid, dim3(T::kThreads), T::kLdsBytes,
+                       s, a);
+    return hipGetLastError();
+}
+
+// Launch shapes (measured on MI355X at M = 512, K = 2048 / 11008):
+//   gate/up: 128 token rows x (4 waves x 16 gate + 16 up rows), 3 waves per SIMD;
+//   plain:    96 token rows x (4 waves x 32 rows), 4 waves per SIMD -- the
+//             N = 2048 projections need the extra blocks more than the reuse.
+using GateUpShape = PrefillTile<8, 2, 4, 2>;
+using PlainShape = PrefillTile<6, 2, 4, 1>;
+
+uint32_t prefill_block_m(bool gate_up) { return gate_up ? GateUpShape::kBM : PlainShape::kBM; }
+uint32_t prefill_block_rows(bool gate_up) { return gate_up ? GateUpShape::kBN : PlainShape::kBN; }
+
+bool prefill_supported(const MfmaArgs &a) {
+    // 32-bit buffer offsets: every operand must span < 4 GiB
+    const uint64_t xbytes = (uint64_t)a.m * a.ldx * 2;
+    if (xbytes >= (1ull << 32)) return false;
+    for (int i = 0; i < a.np; ++i) {
+        const uint64_t qbytes = (uint64_t)a.p[i].w.n * (a.k / 2);
+        if (qbytes >= (1ull << 32)) return false;
+    }
+    return a.m > 16 && a.k % 64 == 0;
+}
+
+hipError_t launch_prefill(MfmaArgs &a, hipStream_t s) {
+    const bool gate_up = a.p[0].w2.qw != nullptr;
+    if (gate_up) return launch_prefill_shape<8, 2, 4, 2, 3>(a, s);
+    return launch_prefill_shape<6, 2, 4, 1, 4>(a, s);
+}
+
+}  // namespace kr

@@ -20,7 +20,7 @@ import numpy as np
 import torch  # must be imported before the library: it loads the HIP runtime both share
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG_DIR, "libkriya_q4.so")
+LIB_PATH = os.environ.get("KRIYA_Q4_LIB") or os.path.join(_PKG_DIR, "libkriya_q4.so")
 
 # C ABI constants (include/kriya_q4.h)
 KR_OK = 0
@@ -28,7 +28,7 @@ KR_E_INVALID, KR_E_SHAPE, KR_E_ALIGN, KR_E_HIP, KR_E_WORKSPACE, KR_E_UNSUPPORTED
 DTYPE_BF16, DTYPE_F32 = 0, 1
 ACT_SWIGLU, ACT_GEGLU, ACT_RELU = 0, 1, 2
 OPT_GEMV_ROWS_PER_WAVE, OPT_GEMV_MAX_BLOCKS, OPT_GEMV_SPLIT_K_CHUNKS = 1, 2, 3
-OPT_GEMV_BLOCK_ROWS, OPT_GEMV_PERSISTENT_BLOCKS, OPT_SKINNY_MAX_BLOCKS = 4, 5, 6
+OPT_GEMV_BLOCK_ROWS, OPT_GEMV_PERSISTENT_BLOCKS, OPT_SKINNY_MAX_BLOCKS, OPT_PREFILL_KERNEL = 4, 5, 6, 7
 
 _lib = None
 

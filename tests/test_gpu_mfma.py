@@ -117,3 +117,54 @@ def test_mlp_batched_split_k_is_deterministic(kq):
         runs.append(h.cpu().numpy())
     assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
     assert_rms_close(runs[0] - O.bf16_to_f32(h0), delta, what="mlp B=16")
+
+
+@pytest.mark.parametrize("m,n,k", [(17, 200, 256), (40, 72, 640), (130, 300, 128)])
+def test_gate_up_prefill_tails(kq, m, n, k):
+    """m > 16 runs the prefill kernel: token-row and weight-row tails that end inside a tile."""
+    s = synth()
+    case(f"prefill gate_up tails m={m} n={n} k={k}")
+    g, u = s.q4_weight(n, k, 2500 + n), s.q4_weight(n, k, 2501 + n)
+    x = s.bf16_normal((m, k), 2502 + m)
+    want = O.q4_gate_up_act(O.Q4Planar(*g), O.Q4Planar(*u), x)
+    a = kq.gate_up_act(q4_dev(kq, g), q4_dev(kq, u), dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy()
+    assert_rms_close(a, want, what=f"gate_up m={m} n={n}")
+    ab = kq.gate_up_act(q4_dev(kq, g), q4_dev(kq, u), dev_bf16(x), out_dtype=kq.DTYPE_BF16)
+    assert_bf16_rounded_close(host_bits(ab), want, rms(want), what=f"gate_up bf16 m={m}")
+
+
+def test_mlp_prefill_split_k(kq):
+    """m = 96: the down projection's few tiles are split over K (f32 partials summed in split order)."""
+    s = synth()
+    case("mlp m=96 hidden 512 inter 1408: prefill kernels with split-K down, deterministic, vs oracle")
+    g, u = s.q4_weight(1408, 512, 2601), s.q4_weight(1408, 512, 2602)
+    d = s.q4_weight(512, 1408, 2603)
+    h0 = s.bf16_normal((96, 512), 2604)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    delta = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), h0)
+    runs = []
+    for _ in range(2):
+        h = torch.from_numpy(O.bf16_to_f32(h0)).cuda()
+        kq.mlp(G, U, D, h, x=dev_bf16(h0))
+        runs.append(h.cpu().numpy())
+    assert np.array_equal(runs[0].view(np.uint32), runs[1].view(np.uint32))
+    assert_rms_close(runs[0] - O.bf16_to_f32(h0), delta, what="mlp m=96")
+
+
+@pytest.mark.parametrize("m", [64, 512])
+def test_prefill_kernels_agree(kq, m):
+    """The register-dequant prefill kernel and the LDS-dequant tiled kernel give the same sums
+    up to f32 summation order."""
+    s = synth()
+    case(f"prefill vs tiled kernel m={m} [2048, 2048]")
+    wq = s.q4_weight(2048, 2048, 2700)
+    x = dev_bf16(s.bf16_normal((m, 2048), 2701))
+    w = q4_dev(kq, wq)
+    lib = kq.lib()
+    try:
+        lib.kr_set_option(kq.OPT_PREFILL_KERNEL, 1)
+        ref = kq.q4_linear(w, x, out_dtype=kq.DTYPE_F32).cpu().numpy()
+    finally:
+        lib.kr_set_option(kq.OPT_PREFILL_KERNEL, 0)
+    got = kq.q4_linear(w, x, out_dtype=kq.DTYPE_F32).cpu().numpy()
+    assert np.max(np.abs(got - ref)) <= 1e-4 * rms(ref)
