@@ -219,6 +219,15 @@ int kr_set_option(int option, int value) {
             if (value < 1) return fail(KR_E_INVALID, "skinny max blocks must be >= 1");
             tuning().skinny_max_blocks = value;
             return ok();
+        case KR_OPT_GEMV_LONG_ROWS:
+            if (value != 0 && value != 4 && value != 8 && value != 16)
+                return fail(KR_E_INVALID, "long rows must be 0, 4, 8 or 16");
+            tuning().gemv_long_rows = value;
+            return ok();
+        case KR_OPT_MLP_FUSED:
+            if (value != 0 && value != 1) return fail(KR_E_INVALID, "mlp fused must be 0 or 1");
+            tuning().mlp_fused = value;
+            return ok();
         case KR_OPT_PREFILL_KERNEL:
             if (value != 0 && value != 1) return fail(KR_E_INVALID, "prefill kernel must be 0 or 1");
             tuning().prefill_kernel = value;
@@ -236,6 +245,8 @@ int kr_get_option(int option) {
         case KR_OPT_GEMV_PERSISTENT_BLOCKS: return tuning().gemv_persistent_blocks;
         case KR_OPT_SKINNY_MAX_BLOCKS: return tuning().skinny_max_blocks;
         case KR_OPT_PREFILL_KERNEL: return tuning().prefill_kernel;
+        case KR_OPT_MLP_FUSED: return tuning().mlp_fused;
+        case KR_OPT_GEMV_LONG_ROWS: return tuning().gemv_long_rows;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -396,6 +407,19 @@ int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matr
         return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
     if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
     uint16_t *act = (uint16_t *)workspace;
+    const uint32_t cus = (uint32_t)device_cus();
+    if (m == 1 && tuning().mlp_fused && mlp_fused_supported(to_mat(gate), to_mat(down), cus)) {
+        FusedMlp f{};
+        f.gate = to_mat(gate);
+        f.up = to_mat(up);
+        f.down = to_mat(down);
+        f.x = x;
+        f.h = h;
+        f.h_f32 = h_dtype == KR_DTYPE_F32;
+        f.activation = activation;
+        f.act = act;
+        return hip_status(launch_mlp_fused(f, cus, (hipStream_t)stream), "kr_q4_mlp (fused)");
+    }
     if (int rc = kr_q4_gate_up_act(gate, up, x, m, act, KR_DTYPE_BF16, activation, stream)) return rc;
     if (m == 1) return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
     // down projection: few N tiles at small m, so K is split over blocks; partials live in the workspace

@@ -152,4 +152,80 @@ __device__ __forceinline__ void tile_epilogue(float tot, int lane, uint32_t t, u
     }
 }
 
+// The persistent wave loop of the m == 1 wave kernel: wave `t0` of `nwaves`
+// takes tiles t0, t0 + nwaves, ...; lane l owns the 16-byte chunks l, l + 64
+// of every row (k <= 64 * 32 * C).  The x operand pairs of the lane's chunks
+// are built once, and the next tile's weights (and the value its epilogue
+// needs) are requested before the current tile is reduced and stored.
+template <int R, int C, int EPI>
+__device__ __forceinline__ void gemv_wave_loop(const Q4Mat &A, const Q4Mat &B, const uint16_t *__restrict__ x,
+                                               const GemvOut &o, uint32_t tiles, uint32_t t0, uint32_t nwaves) {
+    constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
+    const int lane = threadIdx.x & (kWave - 1);
+    uint32_t t = t0;
+    const uint32_t nchunks = A.k >> 5;
+    const uint32_t kMask = sgpr_const(0x000F000Fu);
+    const uint32_t kMagic = vgpr_const(0x43004300u);
+    const uint32_t kSelLo = sgpr_const(0x05040100u);
+    const uint32_t kSelHi = sgpr_const(0x07060302u);
+    if (t >= tiles) return;
+
+    // lane's chunks (c < nchunks is lane-dependent only through c = lane + 64 i)
+    XChunk xc[C];
+    bool live[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        const uint32_t c = lane + kWave * i;
+        live[i] = c < nchunks;
+        if (live[i]) load_xchunk(xc[i], x, c, kSelLo, kSelHi);
+    }
+
+    const u32x4 *rq[R];
+    const uint16_t *rs[R];
+    const uint16_t *rb[R];
+    u32x4 wv[C][R];
+    uint32_t sv[C][R], bv[C][R];
+    auto fetch = [&](uint32_t tt) {
+        tile_rows<R, kGateUp>(A, B, tt, rq, rs, rb);
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+            const uint32_t c = lane + kWave * i;
+            if (live[i]) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    wv[i][r] = ld_stream(rq[r] + c);
+                    sv[i][r] = ld_stream(rs[r] + (c >> 1));
+                    bv[i][r] = ld_stream(rb[r] + (c >> 1));
+                }
+            }
+        }
+    };
+    fetch(t);
+    float pre = tile_prefetch<R, EPI>(lane, t, A.n, o);
+    for (;;) {
+        // consume the fetched tile into accumulators, then prefetch the next one
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+            if (live[i]) {
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r] = chunk_dot(wv[i][r], sv[i][r], bv[i][r], xc[i], acc[r], kMask, kMagic);
+            }
+        }
+        const uint32_t tn = t + nwaves;
+        float pre_n = 0.0f;
+        if (tn < tiles) {
+            fetch(tn);
+            pre_n = tile_prefetch<R, EPI>(lane, tn, A.n, o);
+        }
+        const float tot = wave_reduce_rows<R>(acc, lane);
+        tile_epilogue<R, EPI>(tot, lane, t, A.n, o, pre);
+        if (tn >= tiles) break;
+        t = tn;
+        pre = pre_n;
+    }
+}
+
 }  // namespace kr

@@ -35,73 +35,8 @@ namespace kr {
 template <int R, int C, int EPI>
 __global__ __launch_bounds__(256) void q4_gemv_wave_kernel(Q4Mat A, Q4Mat B, const uint16_t *__restrict__ x,
                                                            GemvOut o, uint32_t tiles) {
-    constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
-    const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t nwaves = gridDim.x * 4;
-    uint32_t t = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const uint32_t nchunks = A.k >> 5;
-    const uint32_t kMask = sgpr_const(0x000F000Fu);
-    const uint32_t kMagic = vgpr_const(0x43004300u);
-    const uint32_t kSelLo = sgpr_const(0x05040100u);
-    const uint32_t kSelHi = sgpr_const(0x07060302u);
-    if (t >= tiles) return;
-
-    // lane's chunks (c < nchunks is lane-dependent only through c = lane + 64 i)
-    XChunk xc[C];
-    bool live[C];
-#pragma unroll
-    for (int i = 0; i < C; ++i) {
-        const uint32_t c = lane + kWave * i;
-        live[i] = c < nchunks;
-        if (live[i]) load_xchunk(xc[i], x, c, kSelLo, kSelHi);
-    }
-
-    const u32x4 *rq[R];
-    const uint16_t *rs[R];
-    const uint16_t *rb[R];
-    u32x4 wv[C][R];
-    uint32_t sv[C][R], bv[C][R];
-    auto fetch = [&](uint32_t tt) {
-        tile_rows<R, kGateUp>(A, B, tt, rq, rs, rb);
-#pragma unroll
-        for (int i = 0; i < C; ++i) {
-            const uint32_t c = lane + kWave * i;
-            if (live[i]) {
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    wv[i][r] = ld_stream(rq[r] + c);
-                    sv[i][r] = ld_stream(rs[r] + (c >> 1));
-                    bv[i][r] = ld_stream(rb[r] + (c >> 1));
-                }
-            }
-        }
-    };
-    fetch(t);
-    float pre = tile_prefetch<R, EPI>(lane, t, A.n, o);
-    for (;;) {
-        // consume the fetched tile into accumulators, then prefetch the next one
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < C; ++i) {
-            if (live[i]) {
-#pragma unroll
-                for (int r = 0; r < R; ++r) acc[r] = chunk_dot(wv[i][r], sv[i][r], bv[i][r], xc[i], acc[r], kMask, kMagic);
-            }
-        }
-        const uint32_t tn = t + nwaves;
-        float pre_n = 0.0f;
-        if (tn < tiles) {
-            fetch(tn);
-            pre_n = tile_prefetch<R, EPI>(lane, tn, A.n, o);
-        }
-        const float tot = wave_reduce_rows<R>(acc, lane);
-        tile_epilogue<R, EPI>(tot, lane, t, A.n, o, pre);
-        if (tn >= tiles) break;
-        t = tn;
-        pre = pre_n;
-    }
+    gemv_wave_loop<R, C, EPI>(A, B, x, o, tiles, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave),
+                              gridDim.x * 4);
 }
 
 // ---------------------------------------------------------------- block (split-K) kernel
@@ -185,6 +120,69 @@ __global__ __launch_bounds__(256) void q4_gemv_block_kernel(Q4Mat A, Q4Mat B, co
     }
 }
 
+// ---------------------------------------------------------------- long-row kernel
+
+// Rows longer than the wave kernel covers (the down projection, k = 11008), up
+// to 512 chunks: one 1024-thread block per RB rows.  Thread (g, c) with row
+// group g = wave / 8 (rows g, g + 2, ..., of the block) and chunk c = 64 (wave
+// mod 8) + lane requests the chunk c of all its rows at once, builds the x
+// pairs of chunk c once and reuses them for those rows -- x is read once per
+// block, not once per row pair -- then the rows are reduced in a fixed order
+// (butterfly, then the 8 waves of the group in order).
+template <int RB, int EPI>
+__global__ __launch_bounds__(1024) void q4_gemv_rows_kernel(Q4Mat A, const uint16_t *__restrict__ x, GemvOut o) {
+    constexpr int RPG = RB / 2;
+    constexpr int kSeg = kWave / RPG;
+    __shared__ float red[2][8][RPG];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const uint32_t g = wave >> 3, c = (wave & 7) * kWave + lane;
+    const uint32_t r0 = blockIdx.x * RB;
+    const uint32_t nchunks = A.k >> 5, wpr = A.k >> 3, groups = A.k >> 6;
+    const uint32_t kMask = sgpr_const(0x000F000Fu);
+    const uint32_t kMagic = vgpr_const(0x43004300u);
+    const uint32_t kSelLo = sgpr_const(0x05040100u);
+    const uint32_t kSelHi = sgpr_const(0x07060302u);
+    float acc[RPG];
+#pragma unroll
+    for (int i = 0; i < RPG; ++i) acc[i] = 0.0f;
+    // the epilogue's operand (old output or bias) of row tid, requested with the weights
+    float pre = 0.0f;
+    if (tid < RB && r0 + tid < A.n) {
+        const uint32_t row = r0 + tid;
+        if (EPI == kAccF32) pre = reinterpret_cast<const float *>(o.out)[row];
+        if (EPI == kAccBF16) pre = bf16_to_f32(reinterpret_cast<const uint16_t *>(o.out)[row]);
+        if ((EPI == kStoreF32 || EPI == kStoreBF16) && o.bias) pre = bf16_to_f32(o.bias[row]);
+    }
+    if (c < nchunks) {
+        u32x4 wv[RPG];
+        uint32_t sv[RPG], bv[RPG];
+#pragma unroll
+        for (int i = 0; i < RPG; ++i) {
+            uint32_t row = r0 + g + 2 * i;
+            row = row < A.n ? row : A.n - 1;  // tail rows re-read a valid row and are never stored
+            wv[i] = ld_stream(reinterpret_cast<const u32x4 *>(A.qw + (size_t)row * wpr) + c);
+            sv[i] = ld_stream(A.sc + (size_t)row * groups + (c >> 1));
+            bv[i] = ld_stream(A.bi + (size_t)row * groups + (c >> 1));
+        }
+        XChunk xc;
+        load_xchunk(xc, x, c, kSelLo, kSelHi);
+#pragma unroll
+        for (int i = 0; i < RPG; ++i) acc[i] = chunk_dot(wv[i], sv[i], bv[i], xc, 0.0f, kMask, kMagic);
+    }
+    const float tot = wave_reduce_rows<RPG>(acc, lane);
+    if ((lane % kSeg) == 0) red[g][wave & 7][lane / kSeg] = tot;
+    __syncthreads();
+    if (tid < RB && r0 + tid < A.n) {
+        const uint32_t gg = tid & 1, slot = tid >> 1;
+        float sum = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) sum += red[gg][w][slot];
+        store_row<EPI>(o, r0 + tid, sum, pre);
+    }
+}
+
 // ---------------------------------------------------------------- launch
 
 template <int EPI>
@@ -229,6 +227,19 @@ template <int EPI>
 static hipError_t launch_epi(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, const GemvOut &o, hipStream_t s) {
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
     const uint32_t chunks = a.k >> 5;
+    const int lr = tuning().gemv_long_rows;
+    if constexpr (!kGateUp) {
+        if (lr > 0 && chunks > 128 && chunks <= 512 && tuning().gemv_split_k_chunks == 0) {
+            const uint32_t blocks = (a.n + lr - 1) / lr;
+            if (lr == 4)
+                hipLaunchKernelGGL((q4_gemv_rows_kernel<4, EPI>), dim3(blocks), dim3(1024), 0, s, a, x, o);
+            else if (lr == 16)
+                hipLaunchKernelGGL((q4_gemv_rows_kernel<16, EPI>), dim3(blocks), dim3(1024), 0, s, a, x, o);
+            else
+                hipLaunchKernelGGL((q4_gemv_rows_kernel<8, EPI>), dim3(blocks), dim3(1024), 0, s, a, x, o);
+            return hipGetLastError();
+        }
+    }
     const int split = tuning().gemv_split_k_chunks;
     const bool use_block = chunks > 128 || (split > 0 && chunks >= (uint32_t)split);
     const int rw = use_block ? tuning().gemv_block_rows : tuning().gemv_rows_per_wave;
