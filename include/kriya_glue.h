@@ -43,6 +43,22 @@ int kr_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16
                         const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
                         uint32_t head_dim, uint32_t max_ctx, uint16_t *out, void *stream);
 
+/* RoPE + KV append + decode attention in two launches: the results of
+ * kr_rope_kv_append followed by kr_attention_decode (up to f32 summation
+ * order), except that q is only read (its rotated copy is not written back).
+ * The context is split into 64-position slices; one block takes a slice of one
+ * sequence for one kv head and all the query heads that share it (GQA), and a
+ * second launch merges the slices in a fixed order.
+ * workspace: kr_attention_workspace_bytes(batch, q_heads, head_dim, max_ctx)
+ * bytes, 16-byte aligned (per-slice partial sums); calls sharing a workspace
+ * must not overlap in time.
+ * Limits: those of kr_attention_decode and q_heads / kv_heads <= 16. */
+size_t kr_attention_workspace_bytes(uint32_t batch, uint32_t q_heads, uint32_t head_dim, uint32_t max_ctx);
+int kr_rope_attention_decode(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *cos_sin,
+                             const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                             uint32_t head_dim, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx,
+                             uint16_t *out, void *workspace, size_t workspace_bytes, void *stream);
+
 /* Greedy sampling (transformer_glue.metal:407-494, temperature 0):
  * out[r] = index of the largest logits[r, :] (ties to the lowest index, NaN never taken). */
 int kr_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, void *stream);

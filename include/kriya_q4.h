@@ -83,8 +83,7 @@ const char *kr_last_error(void);
 #define KR_OPT_GEMV_PERSISTENT_BLOCKS 5 /* grid of the persistent wave kernel (1024)       */
 #define KR_OPT_SKINNY_MAX_BLOCKS 6      /* grid cap of the few-token kernel (512)          */
 #define KR_OPT_PREFILL_KERNEL 7         /* m > 16: 0 register-dequant (default), 1 tiled */
-#define KR_OPT_MLP_FUSED 8              /* m == 1 MLP: 1 single launch, 0 two (default)   */
-#define KR_OPT_GEMV_LONG_ROWS 9         /* k > 4096 rows per 1024-thread block: 4, 8 (default), 16; 0 split-K */
+#define KR_OPT_GEMV_LONG_ROWS 8         /* k > 4096 rows per 1024-thread block: 4, 8 (default), 16; 0 split-K */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 

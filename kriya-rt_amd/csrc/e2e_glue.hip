@@ -232,6 +232,334 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(
     }
 }
 
+// ---- RoPE + KV append + decode attention, split over the context
+//
+// attention_split_kernel<GP>: grid (splits, kv_heads, batch), 256 threads.  The
+// block owns 16 positions of one sequence and one kv head and all G <= GP
+// query heads that share it (GQA: each key and value row is read once for the
+// G heads).  Thread t is lane c = t % 16 of row r = t / 16.  It
+//   0. requests, before anything else, its key piece (position r, dims 8c..)
+//      and its value piece (position c, dims 8r..) -- the rows of D > 128 in a
+//      second piece each;
+//   1. rotates the G query heads (bf16-rounded, as kr_rope_kv_append stores
+//      them) into LDS;
+//   2. if the block holds the new position, rotates k and writes k and v into
+//      the cache (kr_rope_kv_append's arithmetic); its own dots take that row
+//      from LDS;
+//   3. scores: the 16 lanes of a row split the key row; their G partial dots
+//      are summed by a transposing butterfly (lane c ends with head c);
+//   4. per head (a row of 16 lanes, one per position): the slice's max m and
+//      sum l of exp(score - m);
+//   5. values: lane c of row r multiplies its value piece by the G
+//      probabilities of position c; the transposing butterfly over the row
+//      leaves lane c with 8 GP / 16 consecutive (head, dim) sums.
+// The partial (m, l, acc) of each (sequence, kv head, slice) goes to the
+// workspace; attention_combine_kernel merges the slices in slice order:
+//   out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,  M = max_s m_s
+// (with the running max of chunks of 64 slices rescaled as chunks are added).
+constexpr uint32_t kSplitLen = 16;   // positions per slice
+
+__device__ __forceinline__ float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// Sum of R values over the 16 lanes of a row, halving the value set per step:
+// lane c ends with the totals of values (R/16) c .. (R/16) c + R/16 - 1
+// (R >= 16), or of value c / (16/R) (R < 16).  Fixed order.
+template <int R>
+__device__ __forceinline__ void row16_reduce(float (&v)[R], uint32_t c) {
+    int mask = 8;
+#pragma unroll
+    for (int half = R / 2; half >= 1 && mask >= 1; half >>= 1, mask >>= 1) {
+        const bool upper = (c & (uint32_t)mask) != 0;
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            const float send = upper ? v[i] : v[i + half];
+            const float keep = upper ? v[i + half] : v[i];
+            v[i] = keep + __shfl_xor(send, mask);
+        }
+    }
+    if constexpr (R < 16) {
+#pragma unroll
+        for (int m = 8 / R; m >= 1; m >>= 1) v[0] += __shfl_xor(v[0], m);
+    }
+}
+
+template <int GP>
+__global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                                              const float *cos_sin, const uint32_t *positions,
+                                                              uint32_t q_heads, uint32_t kv_heads, uint32_t D,
+                                                              uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx,
+                                                              float *part) {
+    __shared__ __align__(16) float qs[GP * kGlueMaxHeadDim];  // rotated q [G][D]
+    __shared__ float sc[GP][kSplitLen];                        // scores, then exp(score - m)
+    __shared__ __align__(16) float knew[kGlueMaxHeadDim];
+    __shared__ __align__(16) uint16_t vnew[kGlueMaxHeadDim];
+    const uint32_t tid = threadIdx.x, r = tid >> 4, c = tid & 15;
+    const uint32_t s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, splits = gridDim.x;
+    const uint32_t G = q_heads / kv_heads, half = D / 2, P = D / 8;
+    const uint32_t p0 = s * kSplitLen;
+    // 0. loads that do not depend on the position, all in one round trip with it: the key piece
+    //    (position p0 + r, piece c [+16]) and value piece (position p0 + c, piece r [+16]) of rows
+    //    below max_ctx, two query pairs per thread, and the new k and v pairs of thread < D/2.
+    const size_t row_stride = (size_t)kv_heads * D;
+    const uint16_t *kbase = k_cache + (((size_t)b * max_ctx + p0) * kv_heads + kvh) * D;
+    const uint16_t *vbase = v_cache + (((size_t)b * max_ctx + p0) * kv_heads + kvh) * D;
+    u32x4 kw[2], vw[2];
+#pragma unroll
+    for (uint32_t j = 0; j < 2; ++j) {
+        kw[j] = u32x4{0, 0, 0, 0};
+        vw[j] = u32x4{0, 0, 0, 0};
+        if (p0 + r < max_ctx && c + 16 * j < P)
+            kw[j] = *reinterpret_cast<const u32x4 *>(kbase + r * row_stride + 8 * (c + 16 * j));
+        if (p0 + c < max_ctx && r + 16 * j < P)
+            vw[j] = *reinterpret_cast<const u32x4 *>(vbase + c * row_stride + 8 * (r + 16 * j));
+    }
+    constexpr uint32_t kQPairs = GP * kGlueMaxHeadDim / 2 / 256;  // query pairs per thread: G * D/2 <= 256 max(kQPairs, 1)
+    uint32_t qraw[kQPairs > 0 ? kQPairs : 1][2];
+#pragma unroll
+    for (uint32_t j = 0; j < (kQPairs > 0 ? kQPairs : 1); ++j) {
+        const uint32_t i = tid + 256 * j, g = i / half, d = i % half;
+        qraw[j][0] = qraw[j][1] = 0;
+        if (i < G * half) {
+            const uint16_t *src = q + ((size_t)b * q_heads + kvh * G + g) * D;
+            qraw[j][0] = src[d];
+            qraw[j][1] = src[d + half];
+        }
+    }
+    uint32_t kn0 = 0, kn1 = 0, vn0 = 0, vn1 = 0;
+    if (tid < half) {
+        const uint16_t *ks = k + ((size_t)b * kv_heads + kvh) * D;
+        const uint16_t *vs = v + ((size_t)b * kv_heads + kvh) * D;
+        kn0 = ks[tid];
+        kn1 = ks[tid + half];
+        vn0 = vs[tid];
+        vn1 = vs[tid + half];
+    }
+    const uint32_t pos = positions[b];
+    const bool append = pos < max_ctx;
+    const uint32_t n = min(pos, max_ctx - 1) + 1;
+    const uint32_t p1 = min(n, p0 + kSplitLen);
+    float *out = part + (((size_t)b * kv_heads + kvh) * splits + s) * (size_t)G * (D + 2);  // m[G], l[G], acc[G][D]
+    if (p0 >= n) {  // nothing of this sequence in the slice
+        if (tid < G) {
+            out[tid] = -INFINITY;
+            out[G + tid] = 0.0f;
+        }
+        return;
+    }
+    const bool has_new = append && pos >= p0 && pos < p1;
+    // 1. the G query heads, rotated at the new position (the table row is the second round trip)
+#pragma unroll
+    for (uint32_t j = 0; j < (kQPairs > 0 ? kQPairs : 1); ++j) {
+        const uint32_t i = tid + 256 * j, g = i / half, d = i % half;
+        if (i < G * half) {
+            float x0 = bf16_to_f32(qraw[j][0]), x1 = bf16_to_f32(qraw[j][1]);
+            if (append) {
+                const float2 t = reinterpret_cast<const float2 *>(cos_sin)[(size_t)pos * half + d];
+                const float r0 = fmaf(x0, t.x, -x1 * t.y), r1 = fmaf(x0, t.y, x1 * t.x);
+                x0 = bf16_round(r0);
+                x1 = bf16_round(r1);
+            }
+            qs[g * D + d] = x0;
+            qs[g * D + d + half] = x1;
+        }
+    }
+    // rows past the sequence (loaded before its length was known) must not reach the sums
+#pragma unroll
+    for (uint32_t j = 0; j < 2; ++j)
+        if (p0 + c >= p1) vw[j] = u32x4{0, 0, 0, 0};
+    // 2. the new key (rotated) and value, into LDS for this block's own use (the cache is written at the end)
+    if (has_new && tid < half) {
+        const float2 t = reinterpret_cast<const float2 *>(cos_sin)[(size_t)pos * half + tid];
+        const float x0 = bf16_to_f32(kn0), x1 = bf16_to_f32(kn1);
+        const uint32_t k0 = f32_to_bf16(fmaf(x0, t.x, -x1 * t.y)), k1 = f32_to_bf16(fmaf(x0, t.y, x1 * t.x));
+        knew[tid] = bf16_to_f32(k0);
+        knew[tid + half] = bf16_to_f32(k1);
+        vnew[tid] = (uint16_t)vn0;
+        vnew[tid + half] = (uint16_t)vn1;
+        kn0 = k0;  // stored to the cache after the last barrier: a barrier waits for the
+        kn1 = k1;  // block's outstanding global stores
+    }
+    __syncthreads();
+    // 3. scores of position p0 + r: lanes split the key row, then the transposing butterfly
+    {
+        float dot[GP];
+#pragma unroll
+        for (int g = 0; g < GP; ++g) dot[g] = 0.0f;
+        const bool fresh = has_new && p0 + r == pos;
+#pragma unroll
+        for (uint32_t j = 0; j < 2; ++j) {
+            const uint32_t pc = c + 16 * j;
+            if (pc < P && p0 + r < p1) {
+                float kf[8] = {__uint_as_float(kw[j].x << 16), __uint_as_float(kw[j].x & 0xFFFF0000u),
+                               __uint_as_float(kw[j].y << 16), __uint_as_float(kw[j].y & 0xFFFF0000u),
+                               __uint_as_float(kw[j].z << 16), __uint_as_float(kw[j].z & 0xFFFF0000u),
+                               __uint_as_float(kw[j].w << 16), __uint_as_float(kw[j].w & 0xFFFF0000u)};
+                if (fresh) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) kf[e] = knew[8 * pc + e];
+                }
+#pragma unroll
+                for (int g = 0; g < GP; ++g) {
+                    if ((uint32_t)g < G) {
+                        const f32x4 qa = *reinterpret_cast<const f32x4 *>(&qs[g * D + 8 * pc]);
+                        const f32x4 qb = *reinterpret_cast<const f32x4 *>(&qs[g * D + 8 * pc + 4]);
+                        float d0 = dot[g];
+                        d0 = fmaf(qa.x, kf[0], d0);
+                        d0 = fmaf(qa.y, kf[1], d0);
+                        d0 = fmaf(qa.z, kf[2], d0);
+                        d0 = fmaf(qa.w, kf[3], d0);
+                        d0 = fmaf(qb.x, kf[4], d0);
+                        d0 = fmaf(qb.y, kf[5], d0);
+                        d0 = fmaf(qb.z, kf[6], d0);
+                        d0 = fmaf(qb.w, kf[7], d0);
+                        dot[g] = d0;
+                    }
+                }
+            }
+        }
+        row16_reduce<GP>(dot, c);
+        // lane c holds head c (GP >= 16) or head c / (16 / GP) (GP < 16, every such lane holds it)
+        const uint32_t g = GP >= 16 ? c : c / (16 / GP);
+        const bool writer = GP >= 16 || (c % (16 / GP)) == 0;
+        if (writer && g < G) sc[g][r] = p0 + r < p1 ? dot[0] * (1.0f / sqrtf((float)D)) : -INFINITY;
+    }
+    __syncthreads();
+    // 4. per head: row r takes head r, lane c position p0 + c
+    float m_keep = 0.0f, l_keep = 0.0f;
+    if (r < G) {
+        const float x = sc[r][c];
+        float m = x;
+#pragma unroll
+        for (int sh = 8; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
+        const float e = x == -INFINITY ? 0.0f : expf(x - m);
+        float l = e;
+#pragma unroll
+        for (int sh = 8; sh >= 1; sh >>= 1) l += __shfl_xor(l, sh);
+        sc[r][c] = e;
+        m_keep = m;
+        l_keep = l;
+    }
+    __syncthreads();
+    // 5. values: lane c (position p0 + c) of row r (piece r [+16]) for the G heads
+    const bool vfresh = has_new && p0 + c == pos;
+    float pr[GP];
+#pragma unroll
+    for (int g = 0; g < GP; ++g) pr[g] = ((uint32_t)g < G && p0 + c < p1) ? sc[g][c] : 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < 2; ++j) {
+        const uint32_t pc = r + 16 * j;
+        if (16 * j >= P) break;  // uniform: rows of D <= 128 need one round
+        u32x4 w = vw[j];
+        if (vfresh && pc < P) w = *reinterpret_cast<const u32x4 *>(&vnew[8 * pc]);
+        const uint32_t W[4] = {w.x, w.y, w.z, w.w};
+        float acc[8 * GP];
+#pragma unroll
+        for (int g = 0; g < GP; ++g) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[8 * g + 2 * e] = pr[g] * __uint_as_float(W[e] << 16);
+                acc[8 * g + 2 * e + 1] = pr[g] * __uint_as_float(W[e] & 0xFFFF0000u);
+            }
+        }
+        row16_reduce<8 * GP>(acc, c);
+        // lane c holds values (GP / 2) c .. : index i = 8 g + e
+        constexpr int kPer = 8 * GP >= 16 ? 8 * GP / 16 : 1;
+        if (pc < P) {
+#pragma unroll
+            for (int t = 0; t < kPer; ++t) {
+                const uint32_t i = (8 * GP >= 16) ? c * kPer + t : c / (16 / (8 * GP));
+                const uint32_t g = i / 8, e = i % 8;
+                const bool writer = 8 * GP >= 16 || (c % (16 / (8 * GP))) == 0;
+                if (writer && g < G) out[2 * G + g * D + 8 * pc + e] = acc[t];
+            }
+        }
+    }
+    // deferred global stores
+    if (r < G && c == 0) {
+        out[r] = m_keep;
+        out[G + r] = l_keep;
+    }
+    if (has_new && tid < half) {
+        const size_t cbase = (((size_t)b * max_ctx + pos) * kv_heads + kvh) * D;
+        k_cache[cbase + tid] = (uint16_t)kn0;
+        k_cache[cbase + tid + half] = (uint16_t)kn1;
+        v_cache[cbase + tid] = (uint16_t)vn0;
+        v_cache[cbase + tid + half] = (uint16_t)vn1;
+    }
+}
+
+// grid (q_heads, batch), 256 threads: merge the slices of one head in slice order.  Every slice
+// publishes (m, l) -- empty slices (-inf, 0) -- so the merge needs no slice count.  Slices are
+// taken in rounds of NI * 32 (NI = 256 / D interleaves): thread t reads (m, l) of slice t of the
+// round and thread (d = t % D, i = t / D) the values of dim d of slices i, i + NI, ... -- all of a
+// round's loads at once.  The round's max, the weights e^(m_s - M) (one slice per thread) and
+// sum_s w_s l_s are block reductions in a fixed order; the value sums run in slice order per
+// interleave, interleaves added in order; earlier rounds are rescaled to the new max.
+__device__ __forceinline__ float block_max256(float v, float *red) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return v;
+}
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = ((red[0] + red[1]) + red[2]) + red[3];
+    __syncthreads();
+    return v;
+}
+
+__global__ __launch_bounds__(256) void attention_combine_kernel(const float *part, uint32_t q_heads,
+                                                                uint32_t kv_heads, uint32_t D, uint32_t splits,
+                                                                uint16_t *out) {
+    constexpr uint32_t kPer = 32;
+    __shared__ float sw[256];
+    __shared__ float red[256];
+    __shared__ float r4[4];
+    const uint32_t h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const uint32_t G = q_heads / kv_heads, kvh = h / G, g = h % G;
+    const float *base = part + ((size_t)b * kv_heads + kvh) * splits * (size_t)G * (D + 2);
+    const size_t stride = (size_t)G * (D + 2);
+    const uint32_t NI = 256 / D, d = tid % D, il = tid / D;
+    const uint32_t round = min(256u, NI * kPer);
+    float M = -INFINITY, L = 0.0f, acc = 0.0f;
+    for (uint32_t s0 = 0; s0 < splits; s0 += round) {
+        const uint32_t cnt = min(round, splits - s0);
+        float a[kPer];
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j) {
+            const uint32_t sj = il + j * NI;
+            a[j] = (il < NI && sj < cnt) ? base[(s0 + sj) * stride + 2 * G + g * D + d] : 0.0f;
+        }
+        const float mt = tid < cnt ? base[(s0 + tid) * stride + g] : -INFINITY;
+        const float lt = tid < cnt ? base[(s0 + tid) * stride + G + g] : 0.0f;
+        const float Mc = fmaxf(M, block_max256(mt, r4));
+        const float wt = mt == -INFINITY ? 0.0f : expf(mt - Mc);
+        sw[tid] = wt;
+        const float Lr = block_sum256(wt * lt, r4);  // also publishes sw
+        float part_acc = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j) {
+            const uint32_t sj = il + j * NI;
+            if (il < NI && sj < cnt) part_acc = fmaf(sw[sj], a[j], part_acc);
+        }
+        if (il < NI) red[tid] = part_acc;
+        __syncthreads();
+        float racc = 0.0f;
+        for (uint32_t i = 0; i < NI; ++i) racc += red[i * D + d];  // interleaves in order
+        const float scale = M == -INFINITY ? 0.0f : expf(M - Mc);
+        acc = fmaf(acc, scale, racc);
+        L = fmaf(L, scale, Lr);
+        M = Mc;
+        __syncthreads();  // sw, red are rewritten by the next round
+    }
+    if (tid < D) out[((size_t)b * q_heads + h) * D + tid] = (uint16_t)f32_to_bf16(acc / L);
+}
+
 // One block (1024 threads) per row: index of the largest logit, ties to the
 // lowest index (NaN never wins).  Rows of n % 4 == 0 are read as float4,
 // eight loads in flight per thread.
@@ -311,6 +639,40 @@ hipError_t launch_attention_decode(const uint16_t *q, const uint16_t *k_cache, c
     hipLaunchKernelGGL(attention_decode_kernel, dim3(q_heads, batch), dim3(kAttnThreads), 0, s, q, k_cache, v_cache,
                        positions,
                        q_heads, kv_heads, D, max_ctx, out);
+    return hipGetLastError();
+}
+
+uint32_t attention_splits(uint32_t max_ctx) { return (max_ctx + kSplitLen - 1) / kSplitLen; }
+
+size_t attention_workspace_bytes(uint32_t batch, uint32_t q_heads, uint32_t D, uint32_t max_ctx) {
+    return (size_t)batch * attention_splits(max_ctx) * q_heads * (D + 2) * sizeof(float);
+}
+
+hipError_t launch_rope_attention(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *cos_sin,
+                                 const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                                 uint32_t D, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx, uint16_t *out,
+                                 float *part, hipStream_t s) {
+    const uint32_t splits = attention_splits(max_ctx);
+    const uint32_t G = q_heads / kv_heads;
+    const dim3 grid(splits, kv_heads, batch);
+#define KR_SPLIT(GP)                                                                                           \
+    hipLaunchKernelGGL(attention_split_kernel<GP>, grid, dim3(256), 0, s, q, k, v, cos_sin, positions, q_heads, \
+                       kv_heads, D, k_cache, v_cache, max_ctx, part)
+    if (G <= 1)
+        KR_SPLIT(1);
+    else if (G <= 2)
+        KR_SPLIT(2);
+    else if (G <= 4)
+        KR_SPLIT(4);
+    else if (G <= 8)
+        KR_SPLIT(8);
+    else
+        KR_SPLIT(16);
+#undef KR_SPLIT
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(q_heads, batch), dim3(256), 0, s, part, q_heads, kv_heads, D,
+                       splits, out);
     return hipGetLastError();
 }
 

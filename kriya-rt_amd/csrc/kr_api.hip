@@ -224,10 +224,6 @@ int kr_set_option(int option, int value) {
                 return fail(KR_E_INVALID, "long rows must be 0, 4, 8 or 16");
             tuning().gemv_long_rows = value;
             return ok();
-        case KR_OPT_MLP_FUSED:
-            if (value != 0 && value != 1) return fail(KR_E_INVALID, "mlp fused must be 0 or 1");
-            tuning().mlp_fused = value;
-            return ok();
         case KR_OPT_PREFILL_KERNEL:
             if (value != 0 && value != 1) return fail(KR_E_INVALID, "prefill kernel must be 0 or 1");
             tuning().prefill_kernel = value;
@@ -245,7 +241,6 @@ int kr_get_option(int option) {
         case KR_OPT_GEMV_PERSISTENT_BLOCKS: return tuning().gemv_persistent_blocks;
         case KR_OPT_SKINNY_MAX_BLOCKS: return tuning().skinny_max_blocks;
         case KR_OPT_PREFILL_KERNEL: return tuning().prefill_kernel;
-        case KR_OPT_MLP_FUSED: return tuning().mlp_fused;
         case KR_OPT_GEMV_LONG_ROWS: return tuning().gemv_long_rows;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
@@ -407,19 +402,6 @@ int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matr
         return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
     if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
     uint16_t *act = (uint16_t *)workspace;
-    const uint32_t cus = (uint32_t)device_cus();
-    if (m == 1 && tuning().mlp_fused && mlp_fused_supported(to_mat(gate), to_mat(down), cus)) {
-        FusedMlp f{};
-        f.gate = to_mat(gate);
-        f.up = to_mat(up);
-        f.down = to_mat(down);
-        f.x = x;
-        f.h = h;
-        f.h_f32 = h_dtype == KR_DTYPE_F32;
-        f.activation = activation;
-        f.act = act;
-        return hip_status(launch_mlp_fused(f, cus, (hipStream_t)stream), "kr_q4_mlp (fused)");
-    }
     if (int rc = kr_q4_gate_up_act(gate, up, x, m, act, KR_DTYPE_BF16, activation, stream)) return rc;
     if (m == 1) return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
     // down projection: few N tiles at small m, so K is split over blocks; partials live in the workspace
@@ -602,6 +584,32 @@ int kr_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16
     return hip_status(launch_attention_decode(q, k_cache, v_cache, positions, batch, q_heads, kv_heads, head_dim,
                                               max_ctx, out, (hipStream_t)stream),
                       "kr_attention_decode");
+}
+
+size_t kr_attention_workspace_bytes(uint32_t batch, uint32_t q_heads, uint32_t head_dim, uint32_t max_ctx) {
+    return attention_workspace_bytes(batch, q_heads, head_dim, max_ctx);
+}
+
+int kr_rope_attention_decode(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *cos_sin,
+                             const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                             uint32_t head_dim, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx,
+                             uint16_t *out, void *workspace, size_t workspace_bytes, void *stream) {
+    if (int rc = check_heads(q_heads, kv_heads, head_dim, max_ctx)) return rc;
+    if (q_heads / kv_heads > kGlueMaxGroup)
+        return fail(KR_E_SHAPE, "q_heads / kv_heads = %u exceeds %u", q_heads / kv_heads, kGlueMaxGroup);
+    if (batch == 0) return ok();
+    if (!q || !k || !v || !cos_sin || !positions || !k_cache || !v_cache || !out)
+        return fail(KR_E_INVALID, "NULL pointer");
+    if (!aligned(k_cache, 16) || !aligned(v_cache, 16)) return fail(KR_E_ALIGN, "k_cache and v_cache must be 16-byte aligned");
+    if (!aligned(cos_sin, 8)) return fail(KR_E_ALIGN, "cos_sin must be 8-byte aligned");
+    if (batch > 65535) return fail(KR_E_SHAPE, "batch=%u exceeds 65535", batch);
+    const size_t need = attention_workspace_bytes(batch, q_heads, head_dim, max_ctx);
+    if (!workspace || workspace_bytes < need)
+        return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
+    return hip_status(launch_rope_attention(q, k, v, cos_sin, positions, batch, q_heads, kv_heads, head_dim, k_cache,
+                                            v_cache, max_ctx, out, (float *)workspace, (hipStream_t)stream),
+                      "kr_rope_attention_decode");
 }
 
 int kr_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, void *stream) {

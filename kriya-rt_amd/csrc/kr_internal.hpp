@@ -32,7 +32,6 @@ struct Tuning {
     int skinny_max_blocks = 512;       // grid cap of the few-token kernel (blocks walk runs of tiles)
     int prefill_kernel = 0;            // m > 16: 0 = register-dequant prefill kernel,
                                        // 1 = LDS-dequant tiled kernel
-    int mlp_fused = 0;                 // m == 1 MLP: 1 = single fused launch when the shape fits, 0 = two launches
     int gemv_long_rows = 8;            // k > 4096: rows per 1024-thread block of the long-row kernels (4, 8, 16);
                                        // 0 = split-K block kernel
 };
@@ -136,22 +135,12 @@ hipError_t launch_attention_decode(const uint16_t *q, const uint16_t *k_cache, c
                                    const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
                                    uint32_t D, uint32_t max_ctx, uint16_t *out, hipStream_t s);
 hipError_t launch_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, hipStream_t s);
-
-// ---- single-launch dense MLP for one token (q4_mlp_fused.hip)
-struct FusedMlp {
-    Q4Mat gate, up, down;
-    const uint16_t *x;      // bf16 [hidden]
-    void *h;                // [hidden] bf16 or f32, accumulated in place
-    int h_f32;
-    int activation;
-    uint16_t *act;          // bf16 [inter] (workspace)
-    uint32_t rpb;           // down rows per block (set by the launcher)
-};
-// Shapes the fused kernel covers with `nblocks` blocks (one per CU).
-bool mlp_fused_supported(const Q4Mat &gate, const Q4Mat &down, uint32_t nblocks);
-hipError_t launch_mlp_fused(FusedMlp a, uint32_t nblocks, hipStream_t s);
-// Grid-barrier waits that gave up since the library was loaded (0 in a healthy run).
-uint32_t mlp_fused_timeouts();
+constexpr uint32_t kGlueMaxGroup = 16;  // query heads per kv head of the split attention
+size_t attention_workspace_bytes(uint32_t batch, uint32_t q_heads, uint32_t D, uint32_t max_ctx);
+hipError_t launch_rope_attention(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *cos_sin,
+                                 const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                                 uint32_t D, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx, uint16_t *out,
+                                 float *part, hipStream_t s);
 
 // y = W x for one token; `b` is the up matrix for the gate/up epilogues;
 // `bias` (bf16 [n] or nullptr) is added by the store epilogues.

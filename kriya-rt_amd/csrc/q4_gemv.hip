@@ -8,14 +8,19 @@
 // Bound: HBM.  Per output row the kernels stream k/2 bytes of nibbles and
 // k/16 bytes of scales+biases once.
 //
-// Two kernels share one inner step (chunk_dot):
+// Three kernels share one inner step (chunk_dot):
 //   * wave kernel, k <= 64 * 32 * C (C = chunks per lane, 1 or 2): a
 //     wavefront owns a tile of R rows; lane l reads the 16-byte chunks l,
 //     l+64 of every row (one global_load_dwordx4 per row per chunk, so a wave
 //     instruction reads 1 KiB of a row contiguously).  Waves are persistent:
 //     the x operand pairs of the lane's chunks are built once, and the next
 //     tile's weights are loaded while the current tile is reduced.
-//   * block kernel (split-K), longer rows (the down projection, k = 11008):
+//   * long-row kernel, 4096 < k <= 16384 (the down projection, k = 11008):
+//     one 1024-thread block per RB rows; thread (g, c) requests chunk c of
+//     its row group's RB/2 rows at once and builds the x pairs of chunk c
+//     once for all of them, so x is read once per RB rows (the split-K block
+//     kernel reads it once per R = 2 rows: 22 KB per 12 KB of weights).
+//   * block kernel (split-K), longer rows or when a split-K threshold is set:
 //     the 256 threads of a block share the chunks of R rows; thread i reads
 //     chunks i, i+256, i+512; the four wave partials are added through LDS.
 //

@@ -29,7 +29,7 @@ DTYPE_BF16, DTYPE_F32 = 0, 1
 ACT_SWIGLU, ACT_GEGLU, ACT_RELU = 0, 1, 2
 OPT_GEMV_ROWS_PER_WAVE, OPT_GEMV_MAX_BLOCKS, OPT_GEMV_SPLIT_K_CHUNKS = 1, 2, 3
 OPT_GEMV_BLOCK_ROWS, OPT_GEMV_PERSISTENT_BLOCKS, OPT_SKINNY_MAX_BLOCKS, OPT_PREFILL_KERNEL = 4, 5, 6, 7
-OPT_MLP_FUSED, OPT_GEMV_LONG_ROWS = 8, 9
+OPT_GEMV_LONG_ROWS = 8
 
 _lib = None
 
@@ -81,6 +81,8 @@ def lib():
             "kr_rope_kv_append": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, u32, vp]),
             "kr_attention_decode": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, vp]),
             "kr_argmax": (i32, [vp, u32, u32, vp, vp]),
+            "kr_attention_workspace_bytes": (sz, [u32, u32, u32, u32]),
+            "kr_rope_attention_decode": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, u32, vp, vp, sz, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -332,6 +334,28 @@ def attention_decode(q, k_cache, v_cache, positions, q_heads, kv_heads, head_dim
         out = torch.empty((batch, q_heads * head_dim), dtype=torch.bfloat16, device=q.device)
     _check(lib().kr_attention_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(positions), batch, q_heads,
                                      kv_heads, head_dim, max_ctx, _ptr(out), _stream(stream)))
+    return out
+
+
+def attention_workspace(batch, q_heads, head_dim, max_ctx, device="cuda") -> torch.Tensor:
+    """Device workspace of rope_attention_decode (per-slice partial sums)."""
+    nbytes = int(lib().kr_attention_workspace_bytes(batch, q_heads, head_dim, max_ctx))
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def rope_attention_decode(q, k, v, cos_sin, positions, q_heads, kv_heads, head_dim, k_cache, v_cache, out=None,
+                          workspace=None, stream=None):
+    """RoPE + KV append + decode attention (q is read, not rotated in place)."""
+    batch = positions.numel()
+    max_ctx = k_cache.shape[1]
+    if out is None:
+        out = torch.empty((batch, q_heads * head_dim), dtype=torch.bfloat16, device=q.device)
+    if workspace is None:
+        workspace = attention_workspace(batch, q_heads, head_dim, max_ctx, device=q.device)
+    _check(lib().kr_rope_attention_decode(_ptr(q), _ptr(k), _ptr(v), _ptr(cos_sin), _ptr(positions), batch, q_heads,
+                                          kv_heads, head_dim, _ptr(k_cache), _ptr(v_cache), max_ctx, _ptr(out),
+                                          _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                          _stream(stream)))
     return out
 
 

@@ -7,7 +7,8 @@ crates/kriya-backend-metal/src/encoder.rs:4880-5484) for a dense Qwen2 layer:
     x = rmsnorm(h, ln1)                              transformer_glue.metal:158-205
     q, k, v = x Wq^T + bq, x Wk^T + bk, x Wv^T + bv  encode_fused_qkv (:2539-2619)
     rope(q, k) at the position; append k, v          paged_gqa_and_deltanet.metal:115-222
-    a = attention(q, K[0..pos], V[0..pos])           GQA decode
+    a = attention(q, K[0..pos], V[0..pos])           GQA decode (one split-context launch + a combine,
+                                                     rope and append fused in)
     h += a Wo^T                                      encode_q4_linear_accumulate (:2497-2536)
     x = rmsnorm(h, ln2)
     h += down(silu(gate x) * up x)                   encode_dense_mlp (:2851-2906)
@@ -27,8 +28,8 @@ from typing import List
 
 import torch
 
-from . import (ACT_SWIGLU, DTYPE_BF16, DTYPE_F32, Q4Matrix, attention_decode, argmax, embedding, lib,
-               mlp, mlp_workspace, q4_linear, qkv, rmsnorm, rope_kv_append)
+from . import (ACT_SWIGLU, DTYPE_BF16, DTYPE_F32, Q4Matrix, argmax, attention_workspace, embedding, lib, mlp,
+               mlp_workspace, q4_linear, qkv, rmsnorm, rope_attention_decode)
 
 
 @dataclasses.dataclass(frozen=True)
@@ -141,6 +142,7 @@ class QwenQ4Decoder:
         self.logits = torch.empty((batch, c.vocab), dtype=torch.float32, device=device)
         self.next = torch.empty(batch, dtype=torch.int32, device=device)
         self.ws = mlp_workspace(batch, c.hidden, c.inter, device=device)
+        self.attn_ws = attention_workspace(batch, c.q_heads, c.head_dim, self.max_ctx, device=device)
 
     def step(self, stream=None) -> torch.Tensor:
         """One greedy decode step at `positions`; returns the next-token buffer."""
@@ -150,10 +152,9 @@ class QwenQ4Decoder:
             rmsnorm(self.h, L.ln1, c.eps, out=self.x, stream=stream)
             qkv(L.q, L.k, L.v, self.x, q_bias=L.bq, k_bias=L.bk, v_bias=L.bv, out_dtype=DTYPE_BF16,
                 outs=(self.q, self.k, self.v), stream=stream)
-            rope_kv_append(self.q, self.k, self.v, self.cos_sin, self.positions, c.q_heads, c.kv_heads, c.head_dim,
-                           L.k_cache, L.v_cache, stream=stream)
-            attention_decode(self.q, L.k_cache, L.v_cache, self.positions, c.q_heads, c.kv_heads, c.head_dim,
-                             out=self.attn, stream=stream)
+            rope_attention_decode(self.q, self.k, self.v, self.cos_sin, self.positions, c.q_heads, c.kv_heads,
+                                  c.head_dim, L.k_cache, L.v_cache, out=self.attn, workspace=self.attn_ws,
+                                  stream=stream)
             q4_linear(L.o, self.attn, y=self.h, accumulate=True, stream=stream)
             rmsnorm(self.h, L.ln2, c.eps, out=self.x, stream=stream)
             mlp(L.gate, L.up, L.down, self.h, x=self.x, activation=ACT_SWIGLU, workspace=self.ws, stream=stream)

@@ -123,6 +123,33 @@ def test_rope_append_and_attention(kq):
         assert np.all(np.abs(got[b] - want) <= np.abs(want) * 2.0 ** -7 + 1e-3 * np.abs(want).max())
 
 
+@pytest.mark.parametrize("B,H,KVH,D,ctx,pos", [(3, 8, 2, 64, 12, [5, 11, 0]), (2, 16, 2, 128, 513, [512, 130]),
+                                               (1, 4, 4, 32, 200, [199]), (2, 32, 2, 128, 70, [64, 70])])
+def test_rope_attention_matches_two_step_path(kq, B, H, KVH, D, ctx, pos):
+    """Split-context attention with fused RoPE/append against kr_rope_kv_append + kr_attention_decode
+    on the same inputs: identical caches, outputs within a few bf16 ulps (f32 summation order differs).
+    The last case has positions >= max_ctx for one sequence (no append, unrotated q, whole cache)."""
+    from kriya_q4 import synth
+    from kriya_q4.qwen_decode import rope_table
+    case(f"rope+attention split B={B} H={H}/{KVH} D={D} ctx={ctx} pos={pos}")
+    q = dev_bf16(synth.bf16_normal((B, H * D), 3320))
+    k = dev_bf16(synth.bf16_normal((B, KVH * D), 3321))
+    v = dev_bf16(synth.bf16_normal((B, KVH * D), 3322))
+    kc0 = dev_bf16(synth.bf16_normal((B, ctx, KVH, D), 3323))
+    vc0 = dev_bf16(synth.bf16_normal((B, ctx, KVH, D), 3324))
+    cs = rope_table(ctx, D, 1e6).cuda()
+    posd = torch.tensor(pos, dtype=torch.int32).cuda()
+    q1, kc1, vc1 = q.clone(), kc0.clone(), vc0.clone()
+    kq.rope_kv_append(q1, k, v, cs, posd, H, KVH, D, kc1, vc1)
+    want = kq.attention_decode(q1, kc1, vc1, posd, H, KVH, D)
+    kc2, vc2 = kc0.clone(), vc0.clone()
+    got = kq.rope_attention_decode(q, k, v, cs, posd, H, KVH, D, kc2, vc2)
+    assert torch.equal(kc1.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16))
+    g, w = got.float().cpu().numpy(), want.float().cpu().numpy()
+    assert np.all(np.abs(g - w) <= np.abs(w) * 2.0 ** -7 + 1e-3 * np.abs(w).max())
+
+
 def test_argmax_ties_and_nan(kq):
     case("argmax")
     x = np.random.default_rng(3).standard_normal((4, 1000)).astype(np.float32)
