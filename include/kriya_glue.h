@@ -11,6 +11,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "kriya_q4.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -42,6 +44,27 @@ int kr_rope_kv_append(uint16_t *q, const uint16_t *k, const uint16_t *v, const f
 int kr_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                         const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
                         uint32_t head_dim, uint32_t max_ctx, uint16_t *out, void *stream);
+
+/* RMSNorm fused into the consumers of its output (the two per-layer norms of a
+ * decode step).  Results are those of kr_rmsnorm into a bf16 buffer followed by
+ * the Q4 call, up to the f32 summation order of mean(x^2).
+ *
+ * qkv(rmsnorm(h)): arguments as kr_q4_qkv, with h bf16 [m, k] and ln_weight bf16
+ * [k].  m == 1 with k <= 4096 is one launch: every wave of the GEMV holds all of
+ * h and normalises its own chunks.  Otherwise the norm goes to xnorm (bf16
+ * [m, k], 16-byte aligned; may be NULL when m == 1 and k <= 4096) first. */
+int kr_rmsnorm_q4_qkv(const uint16_t *h, const uint16_t *ln_weight, float eps, const kr_q4_matrix *q,
+                      const kr_q4_matrix *k, const kr_q4_matrix *v, const uint16_t *q_bias, const uint16_t *k_bias,
+                      const uint16_t *v_bias, uint32_t m, void *q_out, void *k_out, void *v_out, int out_dtype,
+                      uint16_t *xnorm, void *stream);
+
+/* h += mlp(rmsnorm(h)) for bf16 h [m, hidden] updated in place (kr_q4_mlp with
+ * x = rmsnorm(h)).  m == 1 with hidden <= 4096: the norm is fused into the
+ * gate/up GEMV.  workspace: kr_rmsnorm_q4_mlp_workspace_bytes(m, hidden, inter). */
+size_t kr_rmsnorm_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermediate);
+int kr_rmsnorm_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, uint16_t *h,
+                      const uint16_t *ln_weight, float eps, uint32_t m, int activation, void *workspace,
+                      size_t workspace_bytes, void *stream);
 
 /* RoPE + KV append + decode attention in two launches: the results of
  * kr_rope_kv_append followed by kr_attention_decode (up to f32 summation

@@ -352,6 +352,11 @@ int kr_q4_qkv(const kr_q4_matrix *q, const kr_q4_matrix *k, const kr_q4_matrix *
     void *outs[3] = {q_out, k_out, v_out};
     if (m == 1) {
         const int epi = out_dtype == KR_DTYPE_F32 ? kStoreF32 : kStoreBF16;
+        if (gemv_batch_supported(q->k)) {  // the three projections in one launch
+            const Q4Mat ms[3] = {to_mat(q), to_mat(k), to_mat(v)};
+            return hip_status(launch_gemv_batch(ms, nullptr, x, outs, biases, 3, epi, 0, nullptr, 0.0f, s),
+                              "kr_q4_qkv");
+        }
         for (int i = 0; i < 3; ++i) {
             const hipError_t e = launch_gemv(to_mat(mats[i]), nullptr, x, outs[i], epi, 0, biases[i], s);
             if (e != hipSuccess) return hip_status(e, "kr_q4_qkv");
@@ -584,6 +589,73 @@ int kr_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16
     return hip_status(launch_attention_decode(q, k_cache, v_cache, positions, batch, q_heads, kv_heads, head_dim,
                                               max_ctx, out, (hipStream_t)stream),
                       "kr_attention_decode");
+}
+
+int kr_rmsnorm_q4_qkv(const uint16_t *h, const uint16_t *ln_weight, float eps, const kr_q4_matrix *q,
+                      const kr_q4_matrix *k, const kr_q4_matrix *v, const uint16_t *q_bias, const uint16_t *k_bias,
+                      const uint16_t *v_bias, uint32_t m, void *q_out, void *k_out, void *v_out, int out_dtype,
+                      uint16_t *xnorm, void *stream) {
+    if (int rc = check_matrix(q, "q")) return rc;
+    if (int rc = check_matrix(k, "k")) return rc;
+    if (int rc = check_matrix(v, "v")) return rc;
+    if (q->k != k->k || q->k != v->k) return fail(KR_E_SHAPE, "q, k, v must share k");
+    if (!valid_dtype(out_dtype)) return fail(KR_E_INVALID, "out_dtype %d invalid", out_dtype);
+    if (m == 0) return ok();
+    if (!h || !ln_weight || !q_out || !k_out || !v_out) return fail(KR_E_INVALID, "NULL pointer");
+    if (!aligned(h, 16) || !aligned(ln_weight, 16)) return fail(KR_E_ALIGN, "h and ln_weight must be 16-byte aligned");
+    const size_t osz = dtype_size(out_dtype);
+    if (!aligned(q_out, osz) || !aligned(k_out, osz) || !aligned(v_out, osz)) return fail(KR_E_ALIGN, "output misaligned");
+    hipStream_t s = (hipStream_t)stream;
+    if (m == 1 && gemv_batch_supported(q->k)) {
+        const Q4Mat ms[3] = {to_mat(q), to_mat(k), to_mat(v)};
+        void *outs[3] = {q_out, k_out, v_out};
+        const uint16_t *biases[3] = {q_bias, k_bias, v_bias};
+        const int epi = out_dtype == KR_DTYPE_F32 ? kStoreF32 : kStoreBF16;
+        return hip_status(launch_gemv_batch(ms, nullptr, h, outs, biases, 3, epi, 0, ln_weight, eps, s),
+                          "kr_rmsnorm_q4_qkv");
+    }
+    if (!xnorm || !aligned(xnorm, 16)) return fail(KR_E_INVALID, "xnorm (16-byte aligned) is required for m > 1");
+    if (int rc = hip_status(launch_rmsnorm(h, ln_weight, m, q->k, eps, xnorm, s), "kr_rmsnorm_q4_qkv")) return rc;
+    return kr_q4_qkv(q, k, v, q_bias, k_bias, v_bias, xnorm, m, q_out, k_out, v_out, out_dtype, stream);
+}
+
+size_t kr_rmsnorm_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermediate) {
+    return kr_q4_mlp_workspace_bytes(m, hidden, intermediate) + round_up((size_t)m * hidden * 2, 256);
+}
+
+int kr_rmsnorm_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, uint16_t *h,
+                      const uint16_t *ln_weight, float eps, uint32_t m, int activation, void *workspace,
+                      size_t workspace_bytes, void *stream) {
+    if (int rc = check_matrix(gate, "gate")) return rc;
+    if (int rc = check_matrix(up, "up")) return rc;
+    if (int rc = check_matrix(down, "down")) return rc;
+    if (gate->n != up->n || gate->k != up->k) return fail(KR_E_SHAPE, "gate and up shapes differ");
+    if (down->k != gate->n || down->n != gate->k)
+        return fail(KR_E_SHAPE, "down [%u,%u] does not match gate/up [%u,%u]", down->n, down->k, gate->n, gate->k);
+    if (!valid_act(activation)) return fail(KR_E_INVALID, "activation %d invalid", activation);
+    if (m == 0) return ok();
+    if (!h || !ln_weight) return fail(KR_E_INVALID, "NULL pointer");
+    if (!aligned(h, 16) || !aligned(ln_weight, 16)) return fail(KR_E_ALIGN, "h and ln_weight must be 16-byte aligned");
+    const size_t need = kr_rmsnorm_q4_mlp_workspace_bytes(m, gate->k, gate->n);
+    if (!workspace || workspace_bytes < need)
+        return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    const size_t mlp_bytes = kr_q4_mlp_workspace_bytes(m, gate->k, gate->n);
+    if (m == 1 && gemv_batch_supported(gate->k)) {
+        // gate/up with the norm fused into the x load, then the accumulating down projection
+        uint16_t *act = (uint16_t *)workspace;
+        const Q4Mat g = to_mat(gate), u = to_mat(up);
+        void *outs[1] = {act};
+        const uint16_t *biases[1] = {nullptr};
+        if (int rc = hip_status(launch_gemv_batch(&g, &u, h, outs, biases, 1, kGateUpBF16, activation, ln_weight, eps, s),
+                                "kr_rmsnorm_q4_mlp"))
+            return rc;
+        return kr_q4_linear(down, act, 1, h, KR_DTYPE_BF16, 1, stream);
+    }
+    uint16_t *xnorm = (uint16_t *)((char *)workspace + mlp_bytes);
+    if (int rc = hip_status(launch_rmsnorm(h, ln_weight, m, gate->k, eps, xnorm, s), "kr_rmsnorm_q4_mlp")) return rc;
+    return kr_q4_mlp(gate, up, down, xnorm, h, KR_DTYPE_BF16, m, activation, workspace, mlp_bytes, stream);
 }
 
 size_t kr_attention_workspace_bytes(uint32_t batch, uint32_t q_heads, uint32_t head_dim, uint32_t max_ctx) {

@@ -142,6 +142,15 @@ hipError_t launch_rope_attention(const uint16_t *q, const uint16_t *k, const uin
                                  uint32_t D, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx, uint16_t *out,
                                  float *part, hipStream_t s);
 
+// One launch of the m == 1 wave kernel over up to three problems sharing x and
+// k (k <= 4096): mats[i] (with up[i] for the gate/up epilogues) -> outs[i]
+// (+ biases[i] for the store epilogues).  ln_w != nullptr: x is RMS-normalised
+// first (kr_rmsnorm's arithmetic).
+bool gemv_batch_supported(uint32_t k);
+hipError_t launch_gemv_batch(const Q4Mat *mats, const Q4Mat *up, const uint16_t *x, void *const *outs,
+                             const uint16_t *const *biases, int np, int epilogue, int act, const uint16_t *ln_w,
+                             float eps, hipStream_t s);
+
 // y = W x for one token; `b` is the up matrix for the gate/up epilogues;
 // `bias` (bf16 [n] or nullptr) is added by the store epilogues.
 hipError_t launch_gemv(const Q4Mat &a, const Q4Mat *b, const uint16_t *x, void *out, int epilogue,

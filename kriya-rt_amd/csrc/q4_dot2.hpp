@@ -34,12 +34,8 @@ struct XChunk {
     float sum;
 };
 
-__device__ __forceinline__ void load_xchunk(XChunk &xc, const uint16_t *__restrict__ x, uint32_t c, uint32_t sel_lo,
-                                            uint32_t sel_hi) {
-    const u32x4 *xv = reinterpret_cast<const u32x4 *>(x) + 4 * c;
-    const u32x4 v0 = xv[0], v1 = xv[1], v2 = xv[2], v3 = xv[3];
-    const uint32_t X[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
-                            v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+// x pairs of one chunk from its 16 words (32 bf16 values, element order).
+__device__ __forceinline__ void build_xchunk(XChunk &xc, const uint32_t (&X)[16], uint32_t sel_lo, uint32_t sel_hi) {
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
         xc.p[4 * w + 0] = __builtin_amdgcn_perm(X[4 * w + 2], X[4 * w + 0], sel_lo);
@@ -51,6 +47,22 @@ __device__ __forceinline__ void load_xchunk(XChunk &xc, const uint16_t *__restri
 #pragma unroll
     for (int i = 0; i < 16; ++i) s = dot2_bf16(X[i], 0x3F803F80u, s);
     xc.sum = s;
+}
+
+__device__ __forceinline__ void load_xwords(uint32_t (&X)[16], const uint16_t *__restrict__ x, uint32_t c) {
+    const u32x4 *xv = reinterpret_cast<const u32x4 *>(x) + 4 * c;
+    const u32x4 v0 = xv[0], v1 = xv[1], v2 = xv[2], v3 = xv[3];
+    const uint32_t W[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
+                            v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) X[i] = W[i];
+}
+
+__device__ __forceinline__ void load_xchunk(XChunk &xc, const uint16_t *__restrict__ x, uint32_t c, uint32_t sel_lo,
+                                            uint32_t sel_hi) {
+    uint32_t X[16];
+    load_xwords(X, x, c);
+    build_xchunk(xc, X, sel_lo, sel_hi);
 }
 
 // acc += s * sum_j (128 + q_j) x_j + (b - 128 s) * sum(x) over one chunk of one row.
@@ -152,18 +164,39 @@ __device__ __forceinline__ void tile_epilogue(float tot, int lane, uint32_t t, u
     }
 }
 
+// Up to three problems that share x and k in one launch of the wave kernel
+// (the Q, K and V projections): tile t belongs to problem i when
+// p[i].tile_begin <= t < p[i + 1].tile_begin.  ln_w != nullptr: x is first
+// RMS-normalised, y = bf16(x * rsqrt(mean(x^2) + eps) * ln_w) as kr_rmsnorm
+// computes it (the wave holds all of x when k <= 64 * 32 * C, so the mean is
+// one wave reduction).
+struct GemvProblem {
+    Q4Mat A, B;          // B: the up matrix of the gate/up epilogues (= A otherwise)
+    GemvOut o;
+    uint32_t tile_begin;
+};
+struct GemvBatch {
+    GemvProblem p[3];
+    int np;
+    uint32_t tiles;
+    const uint16_t *ln_w;
+    float eps;
+};
+
 // The persistent wave loop of the m == 1 wave kernel: wave `t0` of `nwaves`
 // takes tiles t0, t0 + nwaves, ...; lane l owns the 16-byte chunks l, l + 64
 // of every row (k <= 64 * 32 * C).  The x operand pairs of the lane's chunks
 // are built once, and the next tile's weights (and the value its epilogue
 // needs) are requested before the current tile is reduced and stored.
 template <int R, int C, int EPI>
-__device__ __forceinline__ void gemv_wave_loop(const Q4Mat &A, const Q4Mat &B, const uint16_t *__restrict__ x,
-                                               const GemvOut &o, uint32_t tiles, uint32_t t0, uint32_t nwaves) {
+__device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16_t *__restrict__ x, uint32_t t0,
+                                               uint32_t nwaves) {
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
     const int lane = threadIdx.x & (kWave - 1);
     uint32_t t = t0;
-    const uint32_t nchunks = A.k >> 5;
+    const uint32_t tiles = gb.tiles;
+    const uint32_t K = gb.p[0].A.k;
+    const uint32_t nchunks = K >> 5;
     const uint32_t kMask = sgpr_const(0x000F000Fu);
     const uint32_t kMagic = vgpr_const(0x43004300u);
     const uint32_t kSelLo = sgpr_const(0x05040100u);
@@ -173,20 +206,64 @@ __device__ __forceinline__ void gemv_wave_loop(const Q4Mat &A, const Q4Mat &B, c
     // lane's chunks (c < nchunks is lane-dependent only through c = lane + 64 i)
     XChunk xc[C];
     bool live[C];
+    uint32_t X[C][16];
 #pragma unroll
     for (int i = 0; i < C; ++i) {
         const uint32_t c = lane + kWave * i;
         live[i] = c < nchunks;
-        if (live[i]) load_xchunk(xc[i], x, c, kSelLo, kSelHi);
+        if (live[i]) load_xwords(X[i], x, c);
     }
+    if (gb.ln_w) {
+        uint32_t Wl[C][16];
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+            if (live[i]) {
+                load_xwords(Wl[i], gb.ln_w, lane + kWave * i);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float a = __uint_as_float(X[i][e] << 16), b = __uint_as_float(X[i][e] & 0xFFFF0000u);
+                    ss = fmaf(a, a, ss);
+                    ss = fmaf(b, b, ss);
+                }
+            }
+        }
+        ss = wave_sum(ss);
+        const float scale = 1.0f / sqrtf(ss / (float)K + gb.eps);
+#pragma unroll
+        for (int i = 0; i < C; ++i) {
+            if (live[i]) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float lo = __uint_as_float(X[i][e] << 16) * scale * __uint_as_float(Wl[i][e] << 16);
+                    const float hi =
+                        __uint_as_float(X[i][e] & 0xFFFF0000u) * scale * __uint_as_float(Wl[i][e] & 0xFFFF0000u);
+                    X[i][e] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < C; ++i)
+        if (live[i]) build_xchunk(xc[i], X[i], kSelLo, kSelHi);
+
+    auto locate = [&](uint32_t tt, uint32_t &lt) -> const GemvProblem & {
+        int pi = 0;
+        if (gb.np > 1 && tt >= gb.p[1].tile_begin) pi = 1;
+        if (gb.np > 2 && tt >= gb.p[2].tile_begin) pi = 2;
+        lt = tt - gb.p[pi].tile_begin;
+        return gb.p[pi];
+    };
 
     const u32x4 *rq[R];
     const uint16_t *rs[R];
     const uint16_t *rb[R];
     u32x4 wv[C][R];
     uint32_t sv[C][R], bv[C][R];
-    auto fetch = [&](uint32_t tt) {
-        tile_rows<R, kGateUp>(A, B, tt, rq, rs, rb);
+    auto fetch = [&](uint32_t tt) -> float {
+        uint32_t lt;
+        const GemvProblem &P = locate(tt, lt);
+        tile_rows<R, kGateUp>(P.A, P.B, lt, rq, rs, rb);
 #pragma unroll
         for (int i = 0; i < C; ++i) {
             const uint32_t c = lane + kWave * i;
@@ -199,9 +276,9 @@ __device__ __forceinline__ void gemv_wave_loop(const Q4Mat &A, const Q4Mat &B, c
                 }
             }
         }
+        return tile_prefetch<R, EPI>(lane, lt, P.A.n, P.o);
     };
-    fetch(t);
-    float pre = tile_prefetch<R, EPI>(lane, t, A.n, o);
+    float pre = fetch(t);
     for (;;) {
         // consume the fetched tile into accumulators, then prefetch the next one
         float acc[R];
@@ -216,12 +293,11 @@ __device__ __forceinline__ void gemv_wave_loop(const Q4Mat &A, const Q4Mat &B, c
         }
         const uint32_t tn = t + nwaves;
         float pre_n = 0.0f;
-        if (tn < tiles) {
-            fetch(tn);
-            pre_n = tile_prefetch<R, EPI>(lane, tn, A.n, o);
-        }
+        if (tn < tiles) pre_n = fetch(tn);
         const float tot = wave_reduce_rows<R>(acc, lane);
-        tile_epilogue<R, EPI>(tot, lane, t, A.n, o, pre);
+        uint32_t lt;
+        const GemvProblem &P = locate(t, lt);
+        tile_epilogue<R, EPI>(tot, lane, lt, P.A.n, P.o, pre);
         if (tn >= tiles) break;
         t = tn;
         pre = pre_n;

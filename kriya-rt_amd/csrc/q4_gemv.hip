@@ -38,9 +38,8 @@ namespace kr {
 // ---------------------------------------------------------------- wave kernel
 
 template <int R, int C, int EPI>
-__global__ __launch_bounds__(256) void q4_gemv_wave_kernel(Q4Mat A, Q4Mat B, const uint16_t *__restrict__ x,
-                                                           GemvOut o, uint32_t tiles) {
-    gemv_wave_loop<R, C, EPI>(A, B, x, o, tiles, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave),
+__global__ __launch_bounds__(256) void q4_gemv_wave_kernel(GemvBatch gb, const uint16_t *__restrict__ x) {
+    gemv_wave_loop<R, C, EPI>(gb, x, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave),
                               gridDim.x * 4);
 }
 
@@ -204,14 +203,27 @@ static uint32_t cap_blocks(uint32_t blocks, uint32_t persistent_default) {
 }
 
 template <int R, int EPI>
-static hipError_t launch_wave(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, const GemvOut &o, hipStream_t s) {
-    const uint32_t tiles = tiles_for<EPI>(a.n, R);
+static hipError_t launch_wave_batch(GemvBatch &gb, const uint16_t *x, hipStream_t s) {
+    uint32_t tiles = 0;
+    for (int i = 0; i < gb.np; ++i) {
+        gb.p[i].tile_begin = tiles;
+        tiles += tiles_for<EPI>(gb.p[i].A.n, R);
+    }
+    gb.tiles = tiles;
     const uint32_t blocks = cap_blocks((tiles + 3) / 4, (uint32_t)tuning().gemv_persistent_blocks);
-    if (a.k <= 64 * 32)
-        hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 1, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, o, tiles);
+    if (gb.p[0].A.k <= 64 * 32)
+        hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 1, EPI>), dim3(blocks), dim3(256), 0, s, gb, x);
     else
-        hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 2, EPI>), dim3(blocks), dim3(256), 0, s, a, b, x, o, tiles);
+        hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 2, EPI>), dim3(blocks), dim3(256), 0, s, gb, x);
     return hipGetLastError();
+}
+
+template <int R, int EPI>
+static hipError_t launch_wave(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, const GemvOut &o, hipStream_t s) {
+    GemvBatch gb{};
+    gb.p[0] = GemvProblem{a, b, o, 0};
+    gb.np = 1;
+    return launch_wave_batch<R, EPI>(gb, x, s);
 }
 
 template <int R, int EPI>
@@ -260,6 +272,39 @@ static hipError_t launch_epi(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, 
             return use_block ? launch_block<8, EPI>(a, b, x, o, s) : launch_wave<8, EPI>(a, b, x, o, s);
         default:
             return use_block ? launch_block<4, EPI>(a, b, x, o, s) : launch_wave<4, EPI>(a, b, x, o, s);
+    }
+}
+
+template <int EPI>
+static hipError_t launch_batch_epi(GemvBatch &gb, const uint16_t *x, hipStream_t s) {
+    switch (tuning().gemv_rows_per_wave) {
+        case 1:
+            if constexpr (EPI == kGateUpF32 || EPI == kGateUpBF16) return launch_wave_batch<2, EPI>(gb, x, s);
+            else return launch_wave_batch<1, EPI>(gb, x, s);
+        case 2: return launch_wave_batch<2, EPI>(gb, x, s);
+        case 8: return launch_wave_batch<8, EPI>(gb, x, s);
+        default: return launch_wave_batch<4, EPI>(gb, x, s);
+    }
+}
+
+bool gemv_batch_supported(uint32_t k) { return k % 64 == 0 && k <= 2 * 64 * 32; }
+
+hipError_t launch_gemv_batch(const Q4Mat *mats, const Q4Mat *up, const uint16_t *x, void *const *outs,
+                             const uint16_t *const *biases, int np, int epilogue, int act, const uint16_t *ln_w,
+                             float eps, hipStream_t s) {
+    GemvBatch gb{};
+    gb.np = np;
+    gb.ln_w = ln_w;
+    gb.eps = eps;
+    for (int i = 0; i < np; ++i) gb.p[i] = GemvProblem{mats[i], up ? up[i] : mats[i], GemvOut{outs[i], biases[i], act}, 0};
+    switch (epilogue) {
+        case kStoreF32: return launch_batch_epi<kStoreF32>(gb, x, s);
+        case kStoreBF16: return launch_batch_epi<kStoreBF16>(gb, x, s);
+        case kAccF32: return launch_batch_epi<kAccF32>(gb, x, s);
+        case kAccBF16: return launch_batch_epi<kAccBF16>(gb, x, s);
+        case kGateUpF32: return launch_batch_epi<kGateUpF32>(gb, x, s);
+        case kGateUpBF16: return launch_batch_epi<kGateUpBF16>(gb, x, s);
+        default: return hipErrorInvalidValue;
     }
 }
 

@@ -82,6 +82,9 @@ def lib():
             "kr_attention_decode": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, vp]),
             "kr_argmax": (i32, [vp, u32, u32, vp, vp]),
             "kr_attention_workspace_bytes": (sz, [u32, u32, u32, u32]),
+            "kr_rmsnorm_q4_qkv": (i32, [vp, vp, ctypes.c_float, M, M, M, vp, vp, vp, u32, vp, vp, vp, i32, vp, vp]),
+            "kr_rmsnorm_q4_mlp_workspace_bytes": (sz, [u32, u32, u32]),
+            "kr_rmsnorm_q4_mlp": (i32, [M, M, M, vp, vp, ctypes.c_float, u32, i32, vp, sz, vp]),
             "kr_rope_attention_decode": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, u32, vp, vp, sz, vp]),
         }
         for name, (res, args) in sig.items():
@@ -239,6 +242,37 @@ def mlp(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, h: torch.Tensor, x: Option
         workspace = mlp_workspace(m, gate.k, gate.n, device=h.device)
     _check(lib().kr_q4_mlp(gate.desc, up.desc, down.desc, _ptr(x), _ptr(h), _dt_of(h), m, activation,
                            _ptr(workspace), workspace.numel(), _stream(stream)))
+    return h
+
+
+def rmsnorm_qkv(h: torch.Tensor, ln_weight: torch.Tensor, eps: float, q: Q4Matrix, k: Q4Matrix, v: Q4Matrix,
+                q_bias=None, k_bias=None, v_bias=None, out_dtype: int = DTYPE_F32, outs=None,
+                xnorm: Optional[torch.Tensor] = None, stream=None):
+    """qkv(rmsnorm(h)): the norm fused into the QKV GEMV at m == 1 (xnorm, bf16 [m, k], is needed for m > 1)."""
+    m = h.numel() // q.k
+    if outs is None:
+        outs = tuple(torch.empty((m, w.n), dtype=_out_dtype(out_dtype), device=h.device) for w in (q, k, v))
+    if xnorm is None and m > 1:
+        xnorm = torch.empty((m, q.k), dtype=torch.bfloat16, device=h.device)
+    _check(lib().kr_rmsnorm_q4_qkv(_ptr(h), _ptr(ln_weight), eps, q.desc, k.desc, v.desc, _ptr(q_bias), _ptr(k_bias),
+                                   _ptr(v_bias), m, _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]), _dt_of(outs[0]),
+                                   _ptr(xnorm), _stream(stream)))
+    return outs
+
+
+def rmsnorm_mlp_workspace(m: int, hidden: int, intermediate: int, device="cuda") -> torch.Tensor:
+    nbytes = int(lib().kr_rmsnorm_q4_mlp_workspace_bytes(m, hidden, intermediate))
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def rmsnorm_mlp(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, h: torch.Tensor, ln_weight: torch.Tensor, eps: float,
+                activation: int = ACT_SWIGLU, workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """h += mlp(rmsnorm(h)) in place for bf16 h."""
+    m = h.numel() // down.n
+    if workspace is None:
+        workspace = rmsnorm_mlp_workspace(m, gate.k, gate.n, device=h.device)
+    _check(lib().kr_rmsnorm_q4_mlp(gate.desc, up.desc, down.desc, _ptr(h), _ptr(ln_weight), eps, m, activation,
+                                   _ptr(workspace), workspace.numel(), _stream(stream)))
     return h
 
 

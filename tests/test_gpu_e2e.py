@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import oracle as O
-from _util import assert_rms_close, dev_bf16, host_bits
+from _util import assert_rms_close, dev_bf16, host_bits, q4_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -148,6 +148,34 @@ def test_rope_attention_matches_two_step_path(kq, B, H, KVH, D, ctx, pos):
     assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16))
     g, w = got.float().cpu().numpy(), want.float().cpu().numpy()
     assert np.all(np.abs(g - w) <= np.abs(w) * 2.0 ** -7 + 1e-3 * np.abs(w).max())
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_rmsnorm_fused_qkv_and_mlp(kq, m):
+    """qkv(rmsnorm(h)) and h += mlp(rmsnorm(h)) against kr_rmsnorm followed by the unfused calls:
+    m = 1 fuses the norm into the GEMVs (the mean may differ in its f32 summation order, so a few
+    normalised values may round to the neighbouring bf16), m = 3 runs the norm first."""
+    from kriya_q4 import synth
+    H, I, QN, KN = 256, 512, 256, 128
+    case(f"rmsnorm fused into qkv / mlp m={m}")
+    h0 = synth.bf16_normal((m, H), 3340)
+    ln = dev_bf16(O.f32_to_bf16(1.0 + O.bf16_to_f32(synth.bf16_normal((H,), 3341, std=0.2))))
+    ws = [q4_dev(kq, synth.q4_weight(n, H, 3342 + i)) for i, n in enumerate((QN, KN, KN))]
+    bs = [dev_bf16(synth.bf16_normal((n,), 3350 + i, std=0.1)) for i, n in enumerate((QN, KN, KN))]
+    h = dev_bf16(h0)
+    x = kq.rmsnorm(h, ln, 1e-6)
+    want = kq.qkv(*ws, x, *bs, out_dtype=kq.DTYPE_F32)
+    got = kq.rmsnorm_qkv(h, ln, 1e-6, *ws, *bs, out_dtype=kq.DTYPE_F32)
+    for g_, w_ in zip(got, want):
+        assert_rms_close(g_.cpu().numpy(), w_.cpu().numpy(), rel=1e-2, what=f"fused qkv m={m}")
+    G, U, D = (q4_dev(kq, synth.q4_weight(n, k, 3360 + i)) for i, (n, k) in enumerate(((I, H), (I, H), (H, I))))
+    h_ref = dev_bf16(h0).clone()
+    kq.mlp(G, U, D, h_ref, x=kq.rmsnorm(h_ref, ln, 1e-6))
+    h_got = dev_bf16(h0).clone()
+    kq.rmsnorm_mlp(G, U, D, h_got, ln, 1e-6)
+    base = O.bf16_to_f32(h0)
+    assert_rms_close(h_got.float().cpu().numpy() - base, h_ref.float().cpu().numpy() - base, rel=1e-2,
+                     what=f"fused mlp m={m}")
 
 
 def test_argmax_ties_and_nan(kq):
