@@ -183,12 +183,39 @@ struct GemvBatch {
     float eps;
 };
 
+template <typename T>
+__device__ __forceinline__ T pick3(int i, T a, T b, T c) {
+    return i == 2 ? c : (i == 1 ? b : a);
+}
+
+// Problem `pi` of the batch (wave-uniform) and tile t's index inside it.
+__device__ __forceinline__ GemvProblem pick_problem(const GemvBatch &gb, int pi, uint32_t t, uint32_t &lt) {
+    const GemvProblem &p0 = gb.p[0], &p1 = gb.p[1], &p2 = gb.p[2];
+    GemvProblem P;
+    P.A.qw = pick3(pi, p0.A.qw, p1.A.qw, p2.A.qw);
+    P.A.sc = pick3(pi, p0.A.sc, p1.A.sc, p2.A.sc);
+    P.A.bi = pick3(pi, p0.A.bi, p1.A.bi, p2.A.bi);
+    P.A.n = pick3(pi, p0.A.n, p1.A.n, p2.A.n);
+    P.A.k = p0.A.k;
+    P.B.qw = pick3(pi, p0.B.qw, p1.B.qw, p2.B.qw);
+    P.B.sc = pick3(pi, p0.B.sc, p1.B.sc, p2.B.sc);
+    P.B.bi = pick3(pi, p0.B.bi, p1.B.bi, p2.B.bi);
+    P.B.n = pick3(pi, p0.B.n, p1.B.n, p2.B.n);
+    P.B.k = p0.A.k;
+    P.o.out = pick3(pi, p0.o.out, p1.o.out, p2.o.out);
+    P.o.bias = pick3(pi, p0.o.bias, p1.o.bias, p2.o.bias);
+    P.o.act = pick3(pi, p0.o.act, p1.o.act, p2.o.act);
+    P.tile_begin = pick3(pi, p0.tile_begin, p1.tile_begin, p2.tile_begin);
+    lt = t - P.tile_begin;
+    return P;
+}
+
 // The persistent wave loop of the m == 1 wave kernel: wave `t0` of `nwaves`
 // takes tiles t0, t0 + nwaves, ...; lane l owns the 16-byte chunks l, l + 64
 // of every row (k <= 64 * 32 * C).  The x operand pairs of the lane's chunks
 // are built once, and the next tile's weights (and the value its epilogue
 // needs) are requested before the current tile is reduced and stored.
-template <int R, int C, int EPI>
+template <int R, int C, int EPI, bool kMulti>
 __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16_t *__restrict__ x, uint32_t t0,
                                                uint32_t nwaves) {
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
@@ -247,12 +274,18 @@ __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16
     for (int i = 0; i < C; ++i)
         if (live[i]) build_xchunk(xc[i], X[i], kSelLo, kSelHi);
 
-    auto locate = [&](uint32_t tt, uint32_t &lt) -> const GemvProblem & {
-        int pi = 0;
-        if (gb.np > 1 && tt >= gb.p[1].tile_begin) pi = 1;
-        if (gb.np > 2 && tt >= gb.p[2].tile_begin) pi = 2;
-        lt = tt - gb.p[pi].tile_begin;
-        return gb.p[pi];
+    // The problem is selected field by field from constant-index reads
+    // (scalar loads and selects).  Indexing the table with a run-time index,
+    // or selecting whole structs, went through per-lane or scratch loads whose
+    // vmcnt waits also waited for the weight prefetch in flight.
+    const int np = gb.np;
+    auto locate = [&](uint32_t tt, uint32_t &lt) -> GemvProblem {
+        if (!kMulti) {
+            lt = tt;
+            return gb.p[0];
+        }
+        const int pi = (np > 2 && tt >= gb.p[2].tile_begin) ? 2 : (np > 1 && tt >= gb.p[1].tile_begin) ? 1 : 0;
+        return pick_problem(gb, pi, tt, lt);
     };
 
     const u32x4 *rq[R];
@@ -262,7 +295,7 @@ __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16
     uint32_t sv[C][R], bv[C][R];
     auto fetch = [&](uint32_t tt) -> float {
         uint32_t lt;
-        const GemvProblem &P = locate(tt, lt);
+        const GemvProblem P = locate(tt, lt);
         tile_rows<R, kGateUp>(P.A, P.B, lt, rq, rs, rb);
 #pragma unroll
         for (int i = 0; i < C; ++i) {
@@ -296,7 +329,7 @@ __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16
         if (tn < tiles) pre_n = fetch(tn);
         const float tot = wave_reduce_rows<R>(acc, lane);
         uint32_t lt;
-        const GemvProblem &P = locate(t, lt);
+        const GemvProblem P = locate(t, lt);
         tile_epilogue<R, EPI>(tot, lane, lt, P.A.n, P.o, pre);
         if (tn >= tiles) break;
         t = tn;

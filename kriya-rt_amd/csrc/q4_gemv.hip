@@ -37,9 +37,11 @@ namespace kr {
 
 // ---------------------------------------------------------------- wave kernel
 
-template <int R, int C, int EPI>
+// kMulti: the batch may hold several problems (np > 1); single-problem
+// launches skip the per-tile problem selection.
+template <int R, int C, int EPI, bool kMulti>
 __global__ __launch_bounds__(256) void q4_gemv_wave_kernel(GemvBatch gb, const uint16_t *__restrict__ x) {
-    gemv_wave_loop<R, C, EPI>(gb, x, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave),
+    gemv_wave_loop<R, C, EPI, kMulti>(gb, x, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave),
                               gridDim.x * 4);
 }
 
@@ -211,10 +213,20 @@ static hipError_t launch_wave_batch(GemvBatch &gb, const uint16_t *x, hipStream_
     }
     gb.tiles = tiles;
     const uint32_t blocks = cap_blocks((tiles + 3) / 4, (uint32_t)tuning().gemv_persistent_blocks);
-    if (gb.p[0].A.k <= 64 * 32)
-        hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 1, EPI>), dim3(blocks), dim3(256), 0, s, gb, x);
-    else
-        hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 2, EPI>), dim3(blocks), dim3(256), 0, s, gb, x);
+    const bool c1 = gb.p[0].A.k <= 64 * 32;
+    if (gb.np == 1) {
+        if (c1)
+            hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 1, EPI, false>), dim3(blocks), dim3(256), 0, s, gb, x);
+        else
+            hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 2, EPI, false>), dim3(blocks), dim3(256), 0, s, gb, x);
+    } else if constexpr (EPI == kStoreF32 || EPI == kStoreBF16) {
+        if (c1)
+            hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 1, EPI, true>), dim3(blocks), dim3(256), 0, s, gb, x);
+        else
+            hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 2, EPI, true>), dim3(blocks), dim3(256), 0, s, gb, x);
+    } else {
+        return hipErrorInvalidValue;  // batches of several problems use the store epilogues only
+    }
     return hipGetLastError();
 }
 
