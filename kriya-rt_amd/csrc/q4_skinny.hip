@@ -9,26 +9,28 @@
 // Bound: HBM (each weight is read once per launch; 16 tokens give AI <= 57 FLOP/B).
 //
 // Mapping.  v_mfma_f32_16x16x32_f16 with A = X (16 token rows, zero-padded)
-// and B = W^T (16 weight rows).  A wave owns whole weight tiles: 16 rows over
-// a K slab of up to NLOAD * 128 columns.  It requests all of a tile's words at
-// once (NLOAD dwordx4 per lane) and multiplies them as they arrive.  Load i of
-// lane group g = lane / 16 reads the 16 bytes of piece 4 i + g of the row
-// (lane l % 16), so one wave instruction reads 64 contiguous bytes of each of
-// 16 rows.  Word j of a piece holds columns 32 (4 i + g) + 8 j .. + 7: that
-// lane's k-block of MFMA slice (i, j).  The matching X fragment comes from LDS,
-// where the block staged the slab's X rows once as fp16 in the order e0 e4 e1
-// e5 e2 e6 e3 e7 of every 8 columns (the order the nibble pairs unpack in), in
-// 16-byte units XOR-swizzled by row so that the 16 rows of a read hit distinct
-// banks.  Scales and biases: lane group g loads the bf16 pairs of groups
-// (2 i, 2 i + 1) for i = 4 g .. 4 g + 3, and slice i takes its pair from lane
-// group i / 4 by a lane shuffle.
+// and B = W^T (16 weight rows).  A block takes a tile of 16 weight rows over a
+// K slab of 2048 columns; wave w multiplies the slab's 128-column pieces
+// 2w, 2w + 1 and the 8 waves' 16 x 16 partial tiles are summed through LDS in
+// wave order (fixed order: results do not depend on timing).  The next tile's
+// words are requested before the current tile is multiplied (two register
+// buffers), and the epilogue's operands (bias, old output) with them, so that
+// no wait on them also waits for the prefetch in flight.  Barriers are
+// LDS-only (s_barrier after an lgkmcnt wait): a fenced barrier would wait for
+// the prefetch.
+// Loads: lane (r16, g) reads 16 bytes of piece p of row r16 (columns 128 p +
+// 32 g .. + 31), so one wave instruction reads 64 contiguous bytes of each of
+// 16 rows.  Word j of those 16 bytes is that lane's k-block of MFMA slice
+// (p, j).  The matching X fragment comes from LDS, where the block staged the
+// slab's X rows once as fp16 in the order e0 e4 e1 e5 e2 e6 e3 e7 of every 8
+// columns (the order the nibble pairs unpack in), in 16-byte units
+// XOR-swizzled by row so that the 16 rows of a read hit distinct banks.
+// Scales and biases: every lane loads the bf16 pair (groups 2p, 2p + 1) of its
+// row and piece and takes the half of its lane group.
 // Dequantisation in registers: nibble pairs (j, j+4) under the fp16 pattern
 // 0x6400 -> exact (1024+q) halves, v_pk_add_f16 -1024, v_pk_fma_f16 (s, b).
-// Waves work independently after the staging barrier: no per-tile barrier, no
-// cross-wave reduction; each lane stores its 4 outputs (rows 4 g + v, column
-// l % 16) directly.
 // Gate/up: a tile holds 8 gate rows (lanes 0-7) and the same 8 up rows (lanes
-// 8-15); the epilogue pairs lane c with lane c + 8.
+// 8-15); the epilogue pairs column c with column c + 8.
 // K longer than one slab is split over blocks (one slab each) and the f32
 // partials are reduced in slab order by q4_mfma_splitk_reduce_kernel.
 // Grouped mode (MoE): the weight matrix stacks E experts of expert_rows rows;
@@ -39,6 +41,7 @@
 // the expert changes.  Experts with more than 16 routed rows are processed in
 // 16-row chunks.
 #include <algorithm>
+#include <type_traits>
 
 #include "kr_internal.hpp"
 
@@ -47,6 +50,8 @@ namespace kr {
 namespace {
 
 constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyPieces = 2;                                // 128-column pieces per wave
+constexpr int kSlabCols = kSkinnyWaves * kSkinnyPieces * 128;  // K columns per block
 
 __device__ __forceinline__ uint32_t opq_s(uint32_t v) {
     uint32_t r;
@@ -96,24 +101,29 @@ __device__ __forceinline__ uint32_t word_of(const u32x4 &v, int i) {
 }
 
 // LDS position of 16-byte X unit u (8 columns) of row r (XOR swizzle by row).
-template <int NLOAD>
+template <int kUnits>
 __device__ __forceinline__ uint32_t xs_index(uint32_t r, uint32_t u) {
-    return r * (NLOAD * 16) + (u ^ r);
+    return r * kUnits + (u ^ r);
 }
 
 }  // namespace
 
-// NLOAD: dwordx4 loads per lane per tile (slab of NLOAD * 128 columns);
+// A block takes a tile of 16 weight rows (gate/up: 8 gate + the same 8 up
+// rows) over a K slab of kSlabCols columns; wave w multiplies the slab's
+// 128-column pieces w * kPieces .. + kPieces - 1 and the 8 waves' 16 x 16
+// partial products are summed through LDS in wave order.
 // kGateUp: interleaved gate/up tiles with the activation epilogue;
 // kGrouped: MoE expert groups.
-template <int NLOAD, bool kGateUp, bool kGrouped>
-__global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void q4_skinny_kernel(
+template <bool kGateUp, bool kGrouped>
+__global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void q4_skinny_kernel(
     SkinnyArgs a) {
     constexpr int NW = kSkinnyWaves;
+    constexpr int KW = kSkinnyPieces;                  // 128-column pieces per wave
     constexpr uint32_t kTileRows = kGateUp ? 8 : 16;  // output features per tile
-    constexpr int kUnits = NLOAD * 16;                // 16-byte X units per LDS row
-    constexpr int kStage = 16 * kUnits / (NW * 64);   // X units staged per thread
-    __shared__ u32x4 xs[16 * kUnits];                 // X slab: 16 rows x NLOAD*128 fp16
+    constexpr int kUnits = NW * KW * 16;               // 16-byte X units per LDS row
+    constexpr int kStage = 16 * kUnits / (NW * 64);    // X units staged per thread
+    __shared__ u32x4 xs[16 * kUnits];                  // X slab: 16 rows x kSlabCols fp16
+    __shared__ float red[2][NW][4][64];                // per-wave partial tiles, double buffered
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -121,8 +131,9 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     const int g = lane >> 4, r16 = lane & 15;
     const uint32_t K = a.k;
     const uint32_t slab = blockIdx.x % a.ksplit;
-    const uint32_t k0 = slab * (NLOAD * 128u);
-    const uint32_t nld = min((uint32_t)NLOAD, (K - k0) >> 7);  // live loads (K % 128 == 0)
+    const uint32_t k0 = slab * (uint32_t)kSlabCols;
+    const uint32_t npieces = min((uint32_t)(NW * KW), (K - k0) >> 7);  // live pieces of the slab (K % 128 == 0)
+    const uint32_t p0 = (uint32_t)wave * KW;                           // this wave's first piece
     const uint32_t kMask = opq_s(0x000F000Fu);
     const uint32_t kMagic = opq_v(0x64006400u);
 
@@ -186,78 +197,93 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     const uint16_t *bi_base = up_lane ? a.w2.bi : a.w.bi;
     const uint32_t kw = K >> 3, kg = K >> 6;
 
-    u32x4 wv[NLOAD];
-    uint32_t sp[4], bp[4];
-    // Words of tile t of expert e.  Loads past the slab (i >= nld) re-read a
-    // live piece and are never multiplied; issuing them keeps every wait on
-    // the words independent of the slab width.
-    auto fetch = [&](uint32_t e, uint32_t t) {
+    // Tile words, double buffered (the buffer index is a compile-time
+    // constant: a run-time index into register arrays becomes moves and
+    // waits).  Pieces past the slab re-read the last live piece and are
+    // multiplied with zero scales and zero X, so that every wait on the words
+    // is independent of the slab width.
+    // The epilogue's operands (bias, old output) of the tile are requested
+    // with its words, so that the epilogue never waits for the next tile's
+    // words in flight.
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    u32x4 wv[2][KW];
+    uint32_t sp[2][KW], bp[2][KW];
+    uint32_t pre_b[2] = {0, 0}, pre_o[2] = {0, 0};  // raw bits: converted at use, not at arrival
+    const uint32_t erow = (uint32_t)tid >> 4, ecol = (uint32_t)tid & 15u;  // epilogue output of threads < 256
+    uint32_t orow = 0;                                                      // its output row (per segment)
+    bool eout = false;                                                      // it stores an output
+    auto fetch = [&](auto BUF, uint32_t e, uint32_t t) {
+        constexpr int b = decltype(BUF)::value;
         uint32_t f = kGateUp ? t * 8 + (r16 & 7) : t * 16 + r16;
         f = f < a.expert_rows ? f : a.expert_rows - 1;  // tail rows re-read a valid row and are never stored
         const size_t row = (size_t)e * a.expert_rows + f;
-        // scales first: their shuffles then never wait for the words
-        // bf16 pairs (groups 2i, 2i+1) for i = 4g .. 4g+3; 4-byte aligned (kg even, scales 4-byte aligned)
+        const u32x4 *src = reinterpret_cast<const u32x4 *>(qw_base + row * kw + (k0 >> 3));
+        // bf16 pairs (groups 2p, 2p+1) of piece p; 4-byte aligned (kg even, scales 4-byte aligned)
         const uint32_t *s32 = reinterpret_cast<const uint32_t *>(sc_base + row * kg + (k0 >> 6));
         const uint32_t *b32 = reinterpret_cast<const uint32_t *>(bi_base + row * kg + (k0 >> 6));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            uint32_t i = 4u * (uint32_t)g + (uint32_t)q;
-            i = i < nld ? i : nld - 1;
-            sp[q] = s32[i];
-            bp[q] = b32[i];
+        for (int i = 0; i < KW; ++i) {
+            uint32_t p = p0 + (uint32_t)i;
+            p = p < npieces ? p : npieces - 1;
+            wv[b][i] = ld_stream(src + 4 * p + g);
+            sp[b][i] = s32[p];
+            bp[b][i] = b32[p];
         }
-        const u32x4 *src = reinterpret_cast<const u32x4 *>(qw_base + row * kw + (k0 >> 3));
-#pragma unroll
-        for (int i = 0; i < NLOAD; ++i) {
-            const uint32_t ii = (uint32_t)i < nld ? (uint32_t)i : nld - 1;
-            wv[i] = ld_stream(src + 4 * ii + g);
-        }
+        // Unconditional loads (threads without an operand read x[0]), so that
+        // no branch makes the compiler wait for them before its join.
+        const uint32_t ef = kGateUp ? t * 8 + (ecol & 7) : t * 16 + ecol;
+        const bool ok = eout && ef < a.expert_rows;
+        const uint16_t *bsrc = (a.bias && ok) ? a.bias + (size_t)e * a.expert_rows + ef : a.x;
+        pre_b[b] = *bsrc;
+        // old output: one aligned u32 (a bf16 output reads the pair holding it)
+        const size_t o = (size_t)orow * a.ldo + ef;
+        const uint32_t *osrc = a.out_f32 ? reinterpret_cast<const uint32_t *>(a.out) + o
+                                         : reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(a.out) +
+                                                                              (o & ~(size_t)1));
+        pre_o[b] = *((a.accumulate && ok) ? osrc : reinterpret_cast<const uint32_t *>(a.x));
     };
 
-    // X rows [base, base + rows) of the slab -> LDS (zeros beyond `rows` and beyond the slab).
-    // All loads are issued before the first conversion.
-    auto stage_x = [&](uint32_t base, uint32_t rows) {
-        uint32_t tid_v = (uint32_t)tid;
-        asm volatile("" : "+v"(tid_v));  // recompute the staging addresses here rather than keep them live
-        // Loads are unconditional (dead units re-read row `base`, unit 0) and
-        // zeroed after, so that no branch splits the batch of loads.
-        u32x4 raw[kStage];
+    // X rows [base, base + rows) of the slab -> LDS (zeros beyond `rows` and
+    // beyond the slab), in two halves: the loads, then (after the caller has
+    // requested the first tile's words) the conversion and LDS stores.
+    // Loads are unconditional (dead units re-read row `base`, unit 0) and
+    // zeroed after, so that no branch splits the batch of loads.
+    u32x4 raw[kStage];
+    auto stage_load = [&](uint32_t base, uint32_t rows) {
 #pragma unroll
         for (int s = 0; s < kStage; ++s) {
-            const uint32_t idx = tid_v + (uint32_t)s * (NW * 64);
+            const uint32_t idx = (uint32_t)tid + (uint32_t)s * (NW * 64);
             const uint32_t r = idx / kUnits, u = idx % kUnits;
-            const bool live = r < rows && u < nld * 16;
+            const bool live = r < rows && u < npieces * 16;
             uint32_t xr = base + (live ? r : 0u);
             if constexpr (kGrouped) {
                 if (a.x_div) xr = a.sorted[xr] / a.x_div;
             }
             raw[s] = *reinterpret_cast<const u32x4 *>(a.x + (size_t)xr * a.ldx + k0 + 8 * (live ? u : 0u));
         }
+    };
+    auto stage_store = [&](uint32_t rows) {
 #pragma unroll
         for (int s = 0; s < kStage; ++s) {
-            const uint32_t idx = tid_v + (uint32_t)s * (NW * 64);
+            const uint32_t idx = (uint32_t)tid + (uint32_t)s * (NW * 64);
             const uint32_t r = idx / kUnits, u = idx % kUnits;
-            const bool live = r < rows && u < nld * 16;
+            const bool live = r < rows && u < npieces * 16;
             const u32x4 z = {0, 0, 0, 0};
-            xs[xs_index<NLOAD>(r, u)] = x_unit(live ? raw[s] : z);
+            xs[xs_index<kUnits>(r, u)] = x_unit(live ? raw[s] : z);
         }
     };
 
-    // X fragment of MFMA slice s = 4 i + j for this lane: unit 16 i + 4 g + j of
-    // row r16, i.e. (swizzle) r16 * kUnits + 16 i + ((4 g + j) ^ r16): one base
-    // per j, and i as an immediate offset.
-    uint32_t xbase[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) xbase[j] = (uint32_t)r16 * kUnits + ((4u * (uint32_t)g + (uint32_t)j) ^ (uint32_t)r16);
-    // LDS byte addresses of the four bases (the low 32 bits of a generic LDS
-    // pointer are its LDS offset).  The reads are issued from inline asm that
-    // waits for them: the compiler cannot hoist all 64 of a tile's reads ahead
-    // of the MFMAs and run out of registers; other waves hide the latency.
+    // X fragment of slice (i, j) of this wave: unit 16 (p0 + i) + 4 g + j of row
+    // r16, i.e. (swizzle) r16 * kUnits + 16 (p0 + i) + ((4 g + j) ^ r16): one
+    // base per j, and i as an immediate offset.  The low 32 bits of a generic
+    // LDS pointer are its LDS offset.
     uint32_t xaddr[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xaddr[j] = (uint32_t)reinterpret_cast<uintptr_t>(&xs[xbase[j]]);
-    // The four X fragments of piece i (slices 4i .. 4i+3) in one batch: four
-    // reads in flight, one wait.
+    for (int j = 0; j < 4; ++j)
+        xaddr[j] = (uint32_t)reinterpret_cast<uintptr_t>(
+            &xs[(uint32_t)r16 * kUnits + 16u * p0 + ((4u * (uint32_t)g + (uint32_t)j) ^ (uint32_t)r16)]);
+    // The four X fragments of piece i in one batch: four reads in flight, one wait.
     auto xread4 = [&](int i, f16x8_t (&x)[4]) {
         u32x4 v0, v1, v2, v3;
         asm volatile(
@@ -274,87 +300,101 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         x[2] = __builtin_bit_cast(f16x8_t, v2);
         x[3] = __builtin_bit_cast(f16x8_t, v3);
     };
+    // LDS-only barrier: the weight prefetch stays in flight across it (a
+    // barrier with a memory fence would wait for every outstanding load).
+    auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
-    auto tile = [&](uint32_t e, uint32_t t, uint32_t base, uint32_t rows) {
-        constexpr int kSlices = NLOAD * 4;
+    // v_perm selector broadcasting this lane's half (group 2p + g/2) of a pair to both halves
+    const uint32_t half_sel = (g >> 1) ? 0x03020302u : 0x01000100u;
+    auto tile_mma = [&](auto BUF) -> f32x4 {
+        constexpr int b = decltype(BUF)::value;
         f32x4 acc = {0, 0, 0, 0};
-        // this lane's bf16 scale/bias pairs (groups 2i, 2i+1 of i = 4g + q) as fp16
-        // pairs; pairs past the slab (i >= nld) become zero, so that those pieces,
-        // which are multiplied too, add exact zeros against zero X (a branch here
-        // would let the compiler sink each piece's load down to its use)
-        uint32_t sh[4], bh[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const bool live = 4u * (uint32_t)g + (uint32_t)q < nld;
-            sh[q] = live ? f16_pair_of_bf16_pair(sp[q]) : 0u;
-            bh[q] = live ? f16_pair_of_bf16_pair(bp[q]) : 0u;
+        for (int i = 0; i < KW; ++i) {
+            const bool live = p0 + (uint32_t)i < npieces;
+            const uint32_t sh = live ? f16_pair_of_bf16_pair(sp[b][i]) : 0u;
+            const uint32_t bh = live ? f16_pair_of_bf16_pair(bp[b][i]) : 0u;
+            const f16x2_t s2 = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0u, sh, half_sel));
+            const f16x2_t b2 = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0u, bh, half_sel));
+            f16x8_t xp[4];
+            xread4(i, xp);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xp[j], w_frag(word_of(wv[b][i], j), s2, b2, kMask, kMagic),
+                                                             acc, 0, 0, 0);
         }
-        // v_perm selector broadcasting this lane's half (group 2i + g/2) of the
-        // second operand to both halves (selector bytes 0-3 pick that operand's bytes)
-        const uint32_t half_sel = (g >> 1) ? 0x03020302u : 0x01000100u;
-        f16x2_t s2 = {}, b2 = {};
-        f16x8_t xp[4];
+        return acc;
+    };
+
+    // ---- epilogue: output (erow, ecol) of the tile, summed over the waves in order
+    int par = 0;
+    auto finish = [&](auto BUF, const f32x4 &acc, uint32_t t) {
+        constexpr int b = decltype(BUF)::value;
 #pragma unroll
-        for (int s = 0; s < kSlices; ++s) {
-            const int i = s / 4, j = s % 4;
-            if (j == 0) xread4(i, xp);
-            if (j == 0) {  // the pairs of piece i live in lane group i / 4
-                const int src = 16 * (i / 4) + r16;
-                const uint32_t spair = __shfl(sh[i % 4], src);
-                const uint32_t bpair = __shfl(bh[i % 4], src);
-                s2 = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0u, spair, half_sel));
-                b2 = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0u, bpair, half_sel));
-            }
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xp[j], w_frag(word_of(wv[i], j), s2, b2, kMask, kMagic), acc,
-                                                         0, 0, 0);
-        }
-        // ---- epilogue: lane holds rows 4g + v of column r16
-        float up[4] = {0, 0, 0, 0};
-        if (kGateUp && !a.partial) {
+        for (int v = 0; v < 4; ++v) red[par][wave][v][lane] = acc[v];
+        lds_barrier();
+        const uint32_t f = kGateUp ? t * 8 + (ecol & 7) : t * 16 + ecol;
+        if (eout && f < a.expert_rows) {
+            const uint32_t L = 16u * (erow >> 2) + ecol, v = erow & 3u;
+            float val = 0.0f;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) up[v] = __shfl_xor(acc[v], 8);
-        }
-        const uint32_t f = kGateUp ? t * 8 + (r16 & 7) : t * 16 + r16;
-        const bool col_live = f < a.expert_rows && (!kGateUp || a.partial || r16 < 8);
-        if (!col_live) return;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const uint32_t row = 4 * g + v;
-            if (row >= rows) continue;
+            for (int w = 0; w < NW; ++w) val += red[par][w][v][L];
             if (a.partial) {  // dense split-K: [ksplit, m, nw * n], gate at f, up at n + f
                 const uint32_t nw = kGateUp ? 2 : 1;
-                float *dst = a.partial + ((size_t)slab * a.m + row) * (size_t)(nw * a.expert_rows);
-                dst[(up_lane ? a.expert_rows : 0u) + f] = acc[v];
-                continue;
-            }
-            float val = acc[v];
-            if (kGateUp) val = activation(val, a.act) * up[v];
-            if (a.bias) val += bf16_to_f32(a.bias[(size_t)e * a.expert_rows + f]);
-            uint32_t orow = base + row;
-            if constexpr (kGrouped) {
-                if (a.out_scatter) orow = a.sorted[orow];
-            }
-            const size_t o = (size_t)orow * a.ldo + f;
-            if (a.out_f32) {
-                float *out = reinterpret_cast<float *>(a.out);
-                out[o] = a.accumulate ? out[o] + val : val;
+                float *dst = a.partial + ((size_t)slab * a.m + erow) * (size_t)(nw * a.expert_rows);
+                dst[((kGateUp && ecol >= 8) ? a.expert_rows : 0u) + f] = val;
             } else {
-                uint16_t *out = reinterpret_cast<uint16_t *>(a.out);
-                out[o] = (uint16_t)f32_to_bf16(a.accumulate ? val + bf16_to_f32(out[o]) : val);
+                if constexpr (kGateUp) {
+                    float up = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < NW; ++w) up += red[par][w][v][L + 8];
+                    val = activation(val, a.act) * up;
+                }
+                if (a.bias) val += bf16_to_f32(pre_b[b]);
+                const size_t o = (size_t)orow * a.ldo + f;
+                if (a.out_f32) {
+                    reinterpret_cast<float *>(a.out)[o] = a.accumulate ? __uint_as_float(pre_o[b]) + val : val;
+                } else {
+                    const uint32_t old = (o & 1) ? pre_o[b] >> 16 : pre_o[b] & 0xFFFFu;
+                    reinterpret_cast<uint16_t *>(a.out)[o] =
+                        (uint16_t)f32_to_bf16(a.accumulate ? val + bf16_to_f32(old) : val);
+                }
             }
+        }
+        par ^= 1;
+    };
+    // Tiles t_begin .. t_end - 1, the first already requested into buffer 0;
+    // each tile's successor is requested before it is multiplied.  The loop
+    // body requests unconditionally and the last one or two tiles are peeled,
+    // so that the compiler's wait counts never assume a skipped request.
+    auto run_tiles = [&](uint32_t e, uint32_t t_begin, uint32_t t_end) {
+        uint32_t t = t_begin;
+        for (; t + 2 < t_end; t += 2) {
+            fetch(B1{}, e, t + 1);
+            finish(B0{}, tile_mma(B0{}), t);
+            fetch(B0{}, e, t + 2);
+            finish(B1{}, tile_mma(B1{}), t + 1);
+        }
+        if (t + 1 < t_end) {
+            fetch(B1{}, e, t + 1);
+            finish(B0{}, tile_mma(B0{}), t);
+            finish(B1{}, tile_mma(B1{}), t + 1);
+        } else {
+            finish(B0{}, tile_mma(B0{}), t);
         }
     };
 
-    // X is staged before the first tile is requested: holding a tile's words
-    // through the staging spills registers, which costs more than the overlap
-    // would save.
     if constexpr (!kGrouped) {  // dense: one X for the whole run
-        stage_x(0, min(a.m, 16u));
-        __syncthreads();
-        for (uint32_t t = run_begin + (uint32_t)wave; t < run_end; t += NW) {
-            fetch(0, t);
-            tile(0, t, 0, a.m);
-        }
+        const uint32_t rows = min(a.m, 16u);
+        eout = tid < 256 && erow < rows && (!kGateUp || a.partial || ecol < 8);
+        orow = erow;
+        // X loads first, then the first tile's words: the conversion waits for X only
+        stage_load(0, rows);
+        fetch(B0{}, 0, run_begin);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_store(rows);
+        lds_barrier();
+        run_tiles(0, run_begin, run_end);
         return;
     }
 
@@ -365,16 +405,19 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         const uint32_t seg_end = min(run_end, (j + 1) * tiles_per_expert);
         uint32_t e, base, cnt;
         expert_of(j, e, base, cnt);
+        const uint32_t t_begin = item - j * tiles_per_expert, t_end = seg_end - j * tiles_per_expert;
         for (uint32_t c0 = 0; c0 < cnt; c0 += 16) {
             const uint32_t rows = min(cnt - c0, 16u);
-            __syncthreads();  // the previous segment's readers are done with xs
-            stage_x(base + c0, rows);
-            __syncthreads();
-            for (uint32_t my = item + (uint32_t)wave; my < seg_end; my += NW) {
-                const uint32_t t = my - j * tiles_per_expert;
-                fetch(e, t);
-                tile(e, t, base + c0, rows);
-            }
+            eout = tid < 256 && erow < rows && (!kGateUp || a.partial || ecol < 8);
+            orow = base + c0 + erow;
+            if (eout && a.out_scatter) orow = a.sorted[orow];
+            stage_load(base + c0, rows);
+            fetch(B0{}, e, t_begin);
+            __builtin_amdgcn_sched_barrier(0);
+            lds_barrier();  // the previous segment's readers are done with xs
+            stage_store(rows);
+            lds_barrier();
+            run_tiles(e, t_begin, t_end);
         }
         item = seg_end;
     }
@@ -382,33 +425,14 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
 
 namespace {
 
-template <int NLOAD, bool GU, bool G>
+template <bool GU, bool G>
 hipError_t launch_t(SkinnyArgs &a, uint32_t items, hipStream_t s) {
     // blocks per slab: every CU busy, each block a contiguous run of ceil(items / nblk) tiles
     const uint32_t cap = std::max<uint32_t>(1, (uint32_t)tuning().skinny_max_blocks / a.ksplit);
     const uint32_t nblk = std::max<uint32_t>(1, std::min(items, cap));
     const dim3 grid(nblk * a.ksplit), block(kSkinnyWaves * 64);
-    hipLaunchKernelGGL((q4_skinny_kernel<NLOAD, GU, G>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((q4_skinny_kernel<GU, G>), grid, block, 0, s, a);
     return hipGetLastError();
-}
-
-template <bool GU, bool G>
-hipError_t launch_nload(SkinnyArgs &a, int nload, uint32_t items, hipStream_t s) {
-    switch (nload) {
-        case 4: return launch_t<4, GU, G>(a, items, s);
-        case 8: return launch_t<8, GU, G>(a, items, s);
-        case 12: return launch_t<12, GU, G>(a, items, s);
-        default: return launch_t<16, GU, G>(a, items, s);
-    }
-}
-
-// Slab width in loads (128 columns each): the smallest instantiated width that
-// covers k, else 16 (2048 columns) with K split over blocks.
-int slab_loads(uint32_t k) {
-    const uint32_t need = k / 128;
-    for (int n : {4, 8, 12, 16})
-        if (need <= (uint32_t)n) return n;
-    return 16;
 }
 
 }  // namespace
@@ -421,8 +445,7 @@ hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s) {
     const bool gate_up = a.w2.qw != nullptr;
     if (!skinny_supported(a.w) || (gate_up && !skinny_supported(a.w2))) return hipErrorInvalidValue;
     const bool grouped = a.offsets != nullptr;
-    const int nload = slab_loads(a.k);
-    a.ksplit = (a.k + nload * 128 - 1) / (nload * 128);
+    a.ksplit = skinny_ksplit(a.k);
     if (grouped && a.ksplit != 1) return hipErrorInvalidValue;
     if (!grouped) {
         a.experts = 1;
@@ -431,15 +454,11 @@ hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s) {
     }
     const uint32_t tile_rows = gate_up ? 8 : 16;
     const uint32_t items = a.max_active * ((a.expert_rows + tile_rows - 1) / tile_rows);
-    if (gate_up)
-        return grouped ? launch_nload<true, true>(a, nload, items, s) : launch_nload<true, false>(a, nload, items, s);
-    return grouped ? launch_nload<false, true>(a, nload, items, s) : launch_nload<false, false>(a, nload, items, s);
+    if (gate_up) return grouped ? launch_t<true, true>(a, items, s) : launch_t<true, false>(a, items, s);
+    return grouped ? launch_t<false, true>(a, items, s) : launch_t<false, false>(a, items, s);
 }
 
-uint32_t skinny_ksplit(uint32_t k) {
-    const int nload = slab_loads(k);
-    return (k + nload * 128 - 1) / (nload * 128);
-}
+uint32_t skinny_ksplit(uint32_t k) { return (k + kSlabCols - 1) / kSlabCols; }
 
 bool skinny_grouped_fits(uint32_t k) { return k % 128 == 0 && skinny_ksplit(k) == 1; }
 
