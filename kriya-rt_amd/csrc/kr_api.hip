@@ -228,6 +228,10 @@ int kr_set_option(int option, int value) {
             if (value != 0 && value != 1) return fail(KR_E_INVALID, "prefill kernel must be 0 or 1");
             tuning().prefill_kernel = value;
             return ok();
+        case KR_OPT_GEMV_TOKENS:
+            if (value != 0 && value != 1) return fail(KR_E_INVALID, "gemv tokens must be 0 or 1");
+            tuning().gemv_tokens = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -242,6 +246,7 @@ int kr_get_option(int option) {
         case KR_OPT_SKINNY_MAX_BLOCKS: return tuning().skinny_max_blocks;
         case KR_OPT_PREFILL_KERNEL: return tuning().prefill_kernel;
         case KR_OPT_GEMV_LONG_ROWS: return tuning().gemv_long_rows;
+        case KR_OPT_GEMV_TOKENS: return tuning().gemv_tokens;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -294,6 +299,11 @@ int kr_q4_linear(const kr_q4_matrix *w, const uint16_t *x, uint32_t m, void *y, 
                                    : (y_dtype == KR_DTYPE_F32 ? kStoreF32 : kStoreBF16);
         return hip_status(launch_gemv(a, nullptr, x, y, epi, 0, nullptr, s), "kr_q4_linear");
     }
+    if (tuning().gemv_tokens && gemv_tokens_supported(m, w->k, false)) {
+        const int epi = accumulate ? (y_dtype == KR_DTYPE_F32 ? kAccF32 : kAccBF16)
+                                   : (y_dtype == KR_DTYPE_F32 ? kStoreF32 : kStoreBF16);
+        return hip_status(launch_gemv_tokens(a, nullptr, x, m, y, w->n, epi, 0, nullptr, s), "kr_q4_linear");
+    }
     if (skinny_fits(m, to_mat(w), false))
         return hip_status(run_skinny(a, nullptr, x, m, y, nullptr, w->n, y_dtype, accumulate, 0, nullptr, s),
                           "kr_q4_linear");
@@ -320,6 +330,11 @@ int kr_q4_gate_up_act(const kr_q4_matrix *gate, const kr_q4_matrix *up, const ui
     if (m == 1) {
         const int epi = act_dtype == KR_DTYPE_F32 ? kGateUpF32 : kGateUpBF16;
         return hip_status(launch_gemv(g, &u, x, act_out, epi, activation, nullptr, s), "kr_q4_gate_up_act");
+    }
+    if (tuning().gemv_tokens && gemv_tokens_supported(m, gate->k, true)) {
+        const int epi = act_dtype == KR_DTYPE_F32 ? kGateUpF32 : kGateUpBF16;
+        return hip_status(launch_gemv_tokens(g, &u, x, m, act_out, gate->n, epi, activation, nullptr, s),
+                          "kr_q4_gate_up_act");
     }
     if (skinny_fits(m, to_mat(gate), false) && skinny_supported(to_mat(up)))
         return hip_status(run_skinny(g, &u, x, m, act_out, nullptr, gate->n, act_dtype, 0, activation, nullptr, s),
@@ -408,7 +423,9 @@ int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matr
     if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
     uint16_t *act = (uint16_t *)workspace;
     if (int rc = kr_q4_gate_up_act(gate, up, x, m, act, KR_DTYPE_BF16, activation, stream)) return rc;
-    if (m == 1) return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
+    if (m == 1 || (tuning().gemv_tokens && gemv_tokens_supported(m, gate->k, true) &&
+                   gemv_tokens_supported(m, down->k, false)))
+        return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
     // down projection: few N tiles at small m, so K is split over blocks; partials live in the workspace
     float *partial = (float *)((char *)workspace + round_up((size_t)m * gate->n * 2, 256));
     if (skinny_fits(m, to_mat(down), true))

@@ -101,6 +101,32 @@ __device__ __forceinline__ float wave_reduce_rows(float (&v)[R], int lane) {
     return s;
 }
 
+// The same over a vector of N values (an SSA value: a float array here was
+// sometimes turned into a memory access with a selected index, which kept it
+// out of registers).
+template <int N>
+struct FVec {
+    typedef float type __attribute__((ext_vector_type(N)));
+};
+template <int N>
+__device__ __forceinline__ float wave_reduce_vec(typename FVec<N>::type v, int lane) {
+#pragma unroll
+    for (int half = N / 2, mask = 32; half >= 1; half >>= 1, mask >>= 1) {
+        const bool upper = (lane & mask) != 0;
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            const float lo = v[i], hi = v[i + half];
+            const float send = upper ? lo : hi;
+            const float keep = upper ? hi : lo;
+            v[i] = keep + __shfl_xor(send, mask);
+        }
+    }
+    float s = v[0];
+#pragma unroll
+    for (int mask = 32 / N; mask >= 1; mask >>= 1) s += __shfl_xor(s, mask);
+    return s;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int mask = 32; mask >= 1; mask >>= 1) v += __shfl_xor(v, mask);

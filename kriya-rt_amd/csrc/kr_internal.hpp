@@ -34,6 +34,8 @@ struct Tuning {
                                        // 1 = LDS-dequant tiled kernel
     int gemv_long_rows = 8;            // k > 4096: rows per 1024-thread block of the long-row kernels (4, 8, 16);
                                        // 0 = split-K block kernel
+    int gemv_tokens = 1;               // 2 <= m <= 4: GEMV kernels over the tokens (1) or the few-token
+                                       // MFMA kernel (0)
 };
 Tuning &tuning();
 
@@ -153,6 +155,13 @@ hipError_t launch_gemv_batch(const Q4Mat *mats, const Q4Mat *up, const uint16_t 
 
 // y = W x for one token; `b` is the up matrix for the gate/up epilogues;
 // `bias` (bf16 [n] or nullptr) is added by the store epilogues.
+// 2 <= m <= kGemvMaxTokens tokens on the GEMV kernels (every unpacked word
+// multiplied with all tokens): k <= 2048, or k <= 16384 without the gate/up
+// epilogue.  Output row t at out + t * ldo elements.
+constexpr uint32_t kGemvMaxTokens = 4;
+bool gemv_tokens_supported(uint32_t m, uint32_t k, bool gate_up);
+hipError_t launch_gemv_tokens(const Q4Mat &a, const Q4Mat *b, const uint16_t *x, uint32_t m, void *out, uint32_t ldo,
+                              int epilogue, int act, const uint16_t *bias, hipStream_t s);
 hipError_t launch_gemv(const Q4Mat &a, const Q4Mat *b, const uint16_t *x, void *out, int epilogue,
                        int activation, const uint16_t *bias, hipStream_t s);
 

@@ -80,11 +80,37 @@ __device__ __forceinline__ float chunk_dot(const u32x4 &wv, uint32_t sraw, uint3
     return fmaf(s, d, fmaf(fmaf(-128.0f, s, b), xc.sum, acc));
 }
 
-// Epilogue operands of the m == 1 kernels.
+// The same for M tokens (x rows of `xc`) sharing the chunk's unpacked words:
+// acc[base + t] += s * D_t + (b - 128 s) * sum(x_t).  M == 1 is chunk_dot.
+// The accumulators are a vector value (a float array here ended up in LDS).
+template <int M, typename V>
+__device__ __forceinline__ void chunk_dot_m(const u32x4 &wv, uint32_t sraw, uint32_t braw, const XChunk (&xc)[M],
+                                            V &acc, int base, uint32_t mask, uint32_t magic) {
+    const float s = bf16_to_f32(sraw);
+    const float b = bf16_to_f32(braw);
+    const float c0 = fmaf(-128.0f, s, b);
+    const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+    uint32_t u[16];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) u[4 * w + j] = ((wd[w] >> (4 * j)) & mask) | magic;
+    }
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+        float d = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) d = dot2_bf16(u[i], xc[t].p[i], d);
+        acc[base + t] = fmaf(s, d, fmaf(c0, xc[t].sum, acc[base + t]));
+    }
+}
+
+// Epilogue operands of the m <= 4 kernels.
 struct GemvOut {
-    void *out;              // [n] (or [channels] for gate/up)
+    void *out;              // [n] (or [channels] for gate/up); token t's row at out + t * ldo
     const uint16_t *bias;   // bf16 [n] added by the store epilogues, or nullptr
     int act;                // activation of the gate/up epilogues
+    uint32_t ldo;           // elements between the output rows of consecutive tokens (M > 1)
 };
 
 template <int EPI>
@@ -133,34 +159,50 @@ __device__ __forceinline__ void tile_rows(const Q4Mat &A, const Q4Mat &B, uint32
     }
 }
 
+// Tokens rounded up to a power of two: the transposing butterfly reduces a
+// power-of-two count of values.
+template <int M>
+constexpr int tokens_pow2() {
+    return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+}
+
+// After wave_reduce_rows<R * MP> over values v = r * MP + token (MP =
+// tokens_pow2<M>(), padded tokens hold zeros), the lanes of segment
+// v = lane / (64 / (R MP)) hold the total of (row r, token).
 // The value store_row needs besides the dot product (bias or old output) of
-// the row this lane stores for tile t; 0 when none.
-template <int R, int EPI>
+// the output this lane stores for tile t; 0 when none.
+template <int R, int EPI, int M = 1>
 __device__ __forceinline__ float tile_prefetch(int lane, uint32_t t, uint32_t nrows, const GemvOut &o) {
-    constexpr int kSeg = kWave / R;
-    const uint32_t row = t * R + (uint32_t)(lane / kSeg);
-    if ((lane % kSeg) != 0 || row >= nrows) return 0.0f;
-    if (EPI == kAccF32) return reinterpret_cast<const float *>(o.out)[row];
-    if (EPI == kAccBF16) return bf16_to_f32(reinterpret_cast<const uint16_t *>(o.out)[row]);
+    constexpr int MP = tokens_pow2<M>();
+    constexpr int kSeg = kWave / (R * MP);
+    const uint32_t v = (uint32_t)(lane / kSeg);
+    const uint32_t row = t * R + v / MP, tok = v % MP;
+    if ((lane % kSeg) != 0 || row >= nrows || tok >= (uint32_t)M) return 0.0f;
+    const size_t idx = (size_t)tok * o.ldo + row;
+    if (EPI == kAccF32) return reinterpret_cast<const float *>(o.out)[idx];
+    if (EPI == kAccBF16) return bf16_to_f32(reinterpret_cast<const uint16_t *>(o.out)[idx]);
     if ((EPI == kStoreF32 || EPI == kStoreBF16) && o.bias) return bf16_to_f32(o.bias[row]);
     return 0.0f;
 }
 
-template <int R, int EPI>
+template <int R, int EPI, int M = 1>
 __device__ __forceinline__ void tile_epilogue(float tot, int lane, uint32_t t, uint32_t nrows, const GemvOut &o,
                                               float pre) {
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
-    constexpr int kSeg = kWave / R;
-    const int slot = lane / kSeg;
+    constexpr int MP = tokens_pow2<M>();
+    constexpr int kSeg = kWave / (R * MP);
+    const uint32_t v = (uint32_t)(lane / kSeg);
+    const uint32_t r = v / MP, tok = v % MP;
+    if (tok >= (uint32_t)M) return;
     if (kGateUp) {
-        const float up = __shfl_xor(tot, kSeg);
-        if ((lane % kSeg) == 0 && (slot & 1) == 0) {
-            const uint32_t ch = t * (R / 2) + (slot >> 1);
-            if (ch < nrows) store_row<EPI>(o, ch, activation(tot, o.act) * up, 0.0f);
+        const float up = __shfl_xor(tot, kWave / R);  // row r + 1 of the same token
+        if ((lane % kSeg) == 0 && (r & 1) == 0) {
+            const uint32_t ch = t * (R / 2) + (r >> 1);
+            if (ch < nrows) store_row<EPI>(o, tok * o.ldo + ch, activation(tot, o.act) * up, 0.0f);
         }
     } else if ((lane % kSeg) == 0) {
-        const uint32_t row = t * R + slot;
-        if (row < nrows) store_row<EPI>(o, row, tot, pre);
+        const uint32_t row = t * R + r;
+        if (row < nrows) store_row<EPI>(o, tok * o.ldo + row, tot, pre);
     }
 }
 
@@ -215,10 +257,13 @@ __device__ __forceinline__ GemvProblem pick_problem(const GemvBatch &gb, int pi,
 // of every row (k <= 64 * 32 * C).  The x operand pairs of the lane's chunks
 // are built once, and the next tile's weights (and the value its epilogue
 // needs) are requested before the current tile is reduced and stored.
-template <int R, int C, int EPI, bool kMulti>
+// M > 1: x holds M token rows of k elements; every unpacked word is
+// multiplied with all of them (no RMSNorm, single problem).
+template <int R, int C, int EPI, bool kMulti, int M = 1>
 __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16_t *__restrict__ x, uint32_t t0,
                                                uint32_t nwaves) {
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
+    static_assert(M == 1 || !kMulti, "several tokens: one problem per launch");
     const int lane = threadIdx.x & (kWave - 1);
     uint32_t t = t0;
     const uint32_t tiles = gb.tiles;
@@ -231,48 +276,9 @@ __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16
     if (t >= tiles) return;
 
     // lane's chunks (c < nchunks is lane-dependent only through c = lane + 64 i)
-    XChunk xc[C];
     bool live[C];
-    uint32_t X[C][16];
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-        const uint32_t c = lane + kWave * i;
-        live[i] = c < nchunks;
-        if (live[i]) load_xwords(X[i], x, c);
-    }
-    if (gb.ln_w) {
-        uint32_t Wl[C][16];
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < C; ++i) {
-            if (live[i]) {
-                load_xwords(Wl[i], gb.ln_w, lane + kWave * i);
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const float a = __uint_as_float(X[i][e] << 16), b = __uint_as_float(X[i][e] & 0xFFFF0000u);
-                    ss = fmaf(a, a, ss);
-                    ss = fmaf(b, b, ss);
-                }
-            }
-        }
-        ss = wave_sum(ss);
-        const float scale = 1.0f / sqrtf(ss / (float)K + gb.eps);
-#pragma unroll
-        for (int i = 0; i < C; ++i) {
-            if (live[i]) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const float lo = __uint_as_float(X[i][e] << 16) * scale * __uint_as_float(Wl[i][e] << 16);
-                    const float hi =
-                        __uint_as_float(X[i][e] & 0xFFFF0000u) * scale * __uint_as_float(Wl[i][e] & 0xFFFF0000u);
-                    X[i][e] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
-                }
-            }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < C; ++i)
-        if (live[i]) build_xchunk(xc[i], X[i], kSelLo, kSelHi);
+    for (int i = 0; i < C; ++i) live[i] = lane + kWave * i < nchunks;
 
     // The problem is selected field by field from constant-index reads
     // (scalar loads and selects).  Indexing the table with a run-time index,
@@ -309,28 +315,87 @@ __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16
                 }
             }
         }
-        return tile_prefetch<R, EPI>(lane, lt, P.A.n, P.o);
+        return tile_prefetch<R, EPI, M>(lane, lt, P.A.n, P.o);
     };
-    float pre = fetch(t);
+
+    XChunk xc[C][M];
+    float pre = 0.0f;
+    if constexpr (M > 1) {
+        // the first tile's words, then every token's x words, all in flight before the first conversion
+        pre = fetch(t);
+        uint32_t X[M][C][16];
+#pragma unroll
+        for (int tk = 0; tk < M; ++tk) {
+#pragma unroll
+            for (int i = 0; i < C; ++i)
+                if (live[i]) load_xwords(X[tk][i], x + (size_t)tk * K, lane + kWave * i);
+        }
+#pragma unroll
+        for (int tk = 0; tk < M; ++tk) {
+#pragma unroll
+            for (int i = 0; i < C; ++i)
+                if (live[i]) build_xchunk(xc[i][tk], X[tk][i], kSelLo, kSelHi);
+        }
+    } else {
+        uint32_t X[C][16];
+#pragma unroll
+        for (int i = 0; i < C; ++i)
+            if (live[i]) load_xwords(X[i], x, lane + kWave * i);
+        if (gb.ln_w) {
+            uint32_t Wl[C][16];
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < C; ++i) {
+                if (live[i]) {
+                    load_xwords(Wl[i], gb.ln_w, lane + kWave * i);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const float a = __uint_as_float(X[i][e] << 16), b = __uint_as_float(X[i][e] & 0xFFFF0000u);
+                        ss = fmaf(a, a, ss);
+                        ss = fmaf(b, b, ss);
+                    }
+                }
+            }
+            ss = wave_sum(ss);
+            const float scale = 1.0f / sqrtf(ss / (float)K + gb.eps);
+#pragma unroll
+            for (int i = 0; i < C; ++i) {
+                if (live[i]) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const float lo = __uint_as_float(X[i][e] << 16) * scale * __uint_as_float(Wl[i][e] << 16);
+                        const float hi =
+                            __uint_as_float(X[i][e] & 0xFFFF0000u) * scale * __uint_as_float(Wl[i][e] & 0xFFFF0000u);
+                        X[i][e] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C; ++i)
+            if (live[i]) build_xchunk(xc[i][0], X[i], kSelLo, kSelHi);
+        pre = fetch(t);
+    }
+
     for (;;) {
         // consume the fetched tile into accumulators, then prefetch the next one
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+        constexpr int MP = tokens_pow2<M>();
+        typename FVec<R * MP>::type acc = {};
 #pragma unroll
         for (int i = 0; i < C; ++i) {
             if (live[i]) {
 #pragma unroll
-                for (int r = 0; r < R; ++r) acc[r] = chunk_dot(wv[i][r], sv[i][r], bv[i][r], xc[i], acc[r], kMask, kMagic);
+                for (int r = 0; r < R; ++r)
+                    chunk_dot_m<M>(wv[i][r], sv[i][r], bv[i][r], xc[i], acc, r * MP, kMask, kMagic);
             }
         }
         const uint32_t tn = t + nwaves;
         float pre_n = 0.0f;
         if (tn < tiles) pre_n = fetch(tn);
-        const float tot = wave_reduce_rows<R>(acc, lane);
+        const float tot = wave_reduce_vec<R * MP>(acc, lane);
         uint32_t lt;
         const GemvProblem P = locate(t, lt);
-        tile_epilogue<R, EPI>(tot, lane, lt, P.A.n, P.o, pre);
+        tile_epilogue<R, EPI, M>(tot, lane, lt, P.A.n, P.o, pre);
         if (tn >= tiles) break;
         t = tn;
         pre = pre_n;

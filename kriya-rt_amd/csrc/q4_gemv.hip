@@ -45,6 +45,15 @@ __global__ __launch_bounds__(256) void q4_gemv_wave_kernel(GemvBatch gb, const u
                               gridDim.x * 4);
 }
 
+// The wave kernel for M = 2..4 tokens (x holds M rows), two rows per tile,
+// k <= 2048; at most 128 VGPRs so that four waves fit per SIMD.
+template <int EPI, int M>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void q4_gemv_tokens_kernel(
+    GemvBatch gb, const uint16_t *__restrict__ x) {
+    gemv_wave_loop<2, 1, EPI, false, M>(gb, x, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave),
+                                        gridDim.x * 4);
+}
+
 // ---------------------------------------------------------------- block (split-K) kernel
 
 template <int R, int C, int EPI>
@@ -135,11 +144,15 @@ __global__ __launch_bounds__(256) void q4_gemv_block_kernel(Q4Mat A, Q4Mat B, co
 // pairs of chunk c once and reuses them for those rows -- x is read once per
 // block, not once per row pair -- then the rows are reduced in a fixed order
 // (butterfly, then the 8 waves of the group in order).
-template <int RB, int EPI>
+// M > 1: x holds M token rows; thread (g, c) multiplies its words with the
+// chunk c of every token and the block stores M rows of outputs.
+template <int RB, int EPI, int M = 1>
 __global__ __launch_bounds__(1024) void q4_gemv_rows_kernel(Q4Mat A, const uint16_t *__restrict__ x, GemvOut o) {
     constexpr int RPG = RB / 2;
-    constexpr int kSeg = kWave / RPG;
-    __shared__ float red[2][8][RPG];
+    constexpr int MP = tokens_pow2<M>();
+    constexpr int kVals = RPG * MP;  // values per thread: (row i of the group, token), tokens padded
+    constexpr int kSeg = kWave / kVals;
+    __shared__ float red[2][8][kVals];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -150,16 +163,16 @@ __global__ __launch_bounds__(1024) void q4_gemv_rows_kernel(Q4Mat A, const uint1
     const uint32_t kMagic = vgpr_const(0x43004300u);
     const uint32_t kSelLo = sgpr_const(0x05040100u);
     const uint32_t kSelHi = sgpr_const(0x07060302u);
-    float acc[RPG];
-#pragma unroll
-    for (int i = 0; i < RPG; ++i) acc[i] = 0.0f;
-    // the epilogue's operand (old output or bias) of row tid, requested with the weights
+    typename FVec<kVals>::type acc = {};
+    // the epilogue's operand (old output or bias) of output tid = (token tid / RB, row tid % RB),
+    // requested with the weights
+    const uint32_t out_row = r0 + (uint32_t)tid % RB, out_tok = (uint32_t)tid / RB;
+    const size_t out_idx = (size_t)out_tok * o.ldo + out_row;
     float pre = 0.0f;
-    if (tid < RB && r0 + tid < A.n) {
-        const uint32_t row = r0 + tid;
-        if (EPI == kAccF32) pre = reinterpret_cast<const float *>(o.out)[row];
-        if (EPI == kAccBF16) pre = bf16_to_f32(reinterpret_cast<const uint16_t *>(o.out)[row]);
-        if ((EPI == kStoreF32 || EPI == kStoreBF16) && o.bias) pre = bf16_to_f32(o.bias[row]);
+    if (tid < RB * M && out_row < A.n) {
+        if (EPI == kAccF32) pre = reinterpret_cast<const float *>(o.out)[out_idx];
+        if (EPI == kAccBF16) pre = bf16_to_f32(reinterpret_cast<const uint16_t *>(o.out)[out_idx]);
+        if ((EPI == kStoreF32 || EPI == kStoreBF16) && o.bias) pre = bf16_to_f32(o.bias[out_row]);
     }
     if (c < nchunks) {
         u32x4 wv[RPG];
@@ -172,20 +185,25 @@ __global__ __launch_bounds__(1024) void q4_gemv_rows_kernel(Q4Mat A, const uint1
             sv[i] = ld_stream(A.sc + (size_t)row * groups + (c >> 1));
             bv[i] = ld_stream(A.bi + (size_t)row * groups + (c >> 1));
         }
-        XChunk xc;
-        load_xchunk(xc, x, c, kSelLo, kSelHi);
+        XChunk xc[M];
+        uint32_t X[M][16];
 #pragma unroll
-        for (int i = 0; i < RPG; ++i) acc[i] = chunk_dot(wv[i], sv[i], bv[i], xc, 0.0f, kMask, kMagic);
+        for (int tk = 0; tk < M; ++tk) load_xwords(X[tk], x + (size_t)tk * A.k, c);
+#pragma unroll
+        for (int tk = 0; tk < M; ++tk) build_xchunk(xc[tk], X[tk], kSelLo, kSelHi);
+#pragma unroll
+        for (int i = 0; i < RPG; ++i) chunk_dot_m<M>(wv[i], sv[i], bv[i], xc, acc, i * MP, kMask, kMagic);
     }
-    const float tot = wave_reduce_rows<RPG>(acc, lane);
+    const float tot = wave_reduce_vec<kVals>(acc, lane);
     if ((lane % kSeg) == 0) red[g][wave & 7][lane / kSeg] = tot;
     __syncthreads();
-    if (tid < RB && r0 + tid < A.n) {
-        const uint32_t gg = tid & 1, slot = tid >> 1;
+    if (tid < RB * M && out_row < A.n) {
+        const uint32_t rr = (uint32_t)tid % RB;
+        const uint32_t gg = rr & 1, v = (rr >> 1) * MP + out_tok;
         float sum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 8; ++w) sum += red[gg][w][slot];
-        store_row<EPI>(o, r0 + tid, sum, pre);
+        for (int w = 0; w < 8; ++w) sum += red[gg][w][v];
+        store_row<EPI>(o, out_idx, sum, pre);
     }
 }
 
@@ -301,6 +319,61 @@ static hipError_t launch_batch_epi(GemvBatch &gb, const uint16_t *x, hipStream_t
 
 bool gemv_batch_supported(uint32_t k) { return k % 64 == 0 && k <= 2 * 64 * 32; }
 
+// ---------------------------------------------------------------- 2 <= m <= 4 tokens
+
+template <int EPI, int M>
+static hipError_t launch_tokens_m(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, const GemvOut &o, hipStream_t s) {
+    constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
+    const uint32_t chunks = a.k >> 5;
+    if (chunks <= 64) {  // one chunk per lane: the wave kernel, two rows per tile
+        GemvBatch gb{};
+        gb.p[0] = GemvProblem{a, b, o, 0};
+        gb.np = 1;
+        gb.tiles = tiles_for<EPI>(a.n, 2);
+        const uint32_t blocks = cap_blocks((gb.tiles + 3) / 4, (uint32_t)tuning().gemv_persistent_blocks);
+        hipLaunchKernelGGL((q4_gemv_tokens_kernel<EPI, M>), dim3(blocks), dim3(256), 0, s, gb, x);
+        return hipGetLastError();
+    }
+    if constexpr (!kGateUp) {
+        if (chunks <= 512) {
+            const uint32_t blocks = (a.n + 7) / 8;
+            hipLaunchKernelGGL((q4_gemv_rows_kernel<8, EPI, M>), dim3(blocks), dim3(1024), 0, s, a, x, o);
+            return hipGetLastError();
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int EPI>
+static hipError_t launch_tokens_epi(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, uint32_t m, const GemvOut &o,
+                                    hipStream_t s) {
+    switch (m) {
+        case 2: return launch_tokens_m<EPI, 2>(a, b, x, o, s);
+        case 3: return launch_tokens_m<EPI, 3>(a, b, x, o, s);
+        case 4: return launch_tokens_m<EPI, 4>(a, b, x, o, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+bool gemv_tokens_supported(uint32_t m, uint32_t k, bool gate_up) {
+    return m >= 2 && m <= kGemvMaxTokens && k % 64 == 0 && (k <= 2048 || (!gate_up && k <= 16384));
+}
+
+hipError_t launch_gemv_tokens(const Q4Mat &a, const Q4Mat *b, const uint16_t *x, uint32_t m, void *out, uint32_t ldo,
+                              int epilogue, int act, const uint16_t *bias, hipStream_t s) {
+    const Q4Mat &bb = b ? *b : a;
+    const GemvOut o{out, bias, act, ldo};
+    switch (epilogue) {
+        case kStoreF32: return launch_tokens_epi<kStoreF32>(a, bb, x, m, o, s);
+        case kStoreBF16: return launch_tokens_epi<kStoreBF16>(a, bb, x, m, o, s);
+        case kAccF32: return launch_tokens_epi<kAccF32>(a, bb, x, m, o, s);
+        case kAccBF16: return launch_tokens_epi<kAccBF16>(a, bb, x, m, o, s);
+        case kGateUpF32: return launch_tokens_epi<kGateUpF32>(a, bb, x, m, o, s);
+        case kGateUpBF16: return launch_tokens_epi<kGateUpBF16>(a, bb, x, m, o, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_gemv_batch(const Q4Mat *mats, const Q4Mat *up, const uint16_t *x, void *const *outs,
                              const uint16_t *const *biases, int np, int epilogue, int act, const uint16_t *ln_w,
                              float eps, hipStream_t s) {
@@ -308,7 +381,7 @@ hipError_t launch_gemv_batch(const Q4Mat *mats, const Q4Mat *up, const uint16_t 
     gb.np = np;
     gb.ln_w = ln_w;
     gb.eps = eps;
-    for (int i = 0; i < np; ++i) gb.p[i] = GemvProblem{mats[i], up ? up[i] : mats[i], GemvOut{outs[i], biases[i], act}, 0};
+    for (int i = 0; i < np; ++i) gb.p[i] = GemvProblem{mats[i], up ? up[i] : mats[i], GemvOut{outs[i], biases[i], act, 0}, 0};
     switch (epilogue) {
         case kStoreF32: return launch_batch_epi<kStoreF32>(gb, x, s);
         case kStoreBF16: return launch_batch_epi<kStoreBF16>(gb, x, s);
@@ -323,7 +396,7 @@ hipError_t launch_gemv_batch(const Q4Mat *mats, const Q4Mat *up, const uint16_t 
 hipError_t launch_gemv(const Q4Mat &a, const Q4Mat *b, const uint16_t *x, void *out, int epilogue, int act,
                        const uint16_t *bias, hipStream_t s) {
     const Q4Mat &bb = b ? *b : a;
-    const GemvOut o{out, bias, act};
+    const GemvOut o{out, bias, act, 0};
     switch (epilogue) {
         case kStoreF32: return launch_epi<kStoreF32>(a, bb, x, o, s);
         case kStoreBF16: return launch_epi<kStoreBF16>(a, bb, x, o, s);

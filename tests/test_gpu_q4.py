@@ -182,6 +182,51 @@ def test_gemv_multi_token_rows(kq):
     assert_rms_close(y, O.q4_matmul(O.Q4Planar(*wq), x), what="m=3")
 
 
+@pytest.mark.parametrize("m", [2, 3, 4])
+@pytest.mark.parametrize("n,k", [(1000, 2048), (37, 128), (129, 1408), (300, 11008), (77, 4160)])
+def test_gemv_tokens_linear(kq, m, n, k):
+    """2 <= m <= 4 on the GEMV kernels (k <= 2048: wave kernel; longer rows: the long-row kernel):
+    all four epilogues against the oracle, and against the few-token MFMA kernel."""
+    s = synth()
+    case(f"linear tokens m={m} n={n} k={k}")
+    wq = s.q4_weight(n, k, 40 + m)
+    x = s.bf16_normal((m, k), 50 + m)
+    want = O.q4_matmul(O.Q4Planar(*wq), x)
+    wd, xd = q4_dev(kq, wq), dev_bf16(x)
+    y = kq.q4_linear(wd, xd, out_dtype=kq.DTYPE_F32).cpu().numpy()
+    assert_rms_close(y, want, what=f"m={m} f32")
+    yb = kq.q4_linear(wd, xd, out_dtype=kq.DTYPE_BF16)
+    assert_bf16_rounded_close(host_bits(yb), want, rms(want), what=f"m={m} bf16")
+    base = s.f32_normal((m, n), 60 + m)
+    acc32 = torch.from_numpy(base.copy()).cuda()
+    kq.q4_linear(wd, xd, y=acc32, accumulate=True)
+    assert_rms_close(acc32.cpu().numpy() - base, want, what=f"m={m} acc f32")
+    base_b = s.bf16_normal((m, n), 70 + m)
+    accb = dev_bf16(base_b).clone()
+    kq.q4_linear(wd, xd, y=accb, accumulate=True)
+    assert_bf16_rounded_close(host_bits(accb), O.bf16_to_f32(base_b) + want, rms(want), what=f"m={m} acc bf16")
+    if k <= 2048:  # the MFMA few-token kernel covers one 2048-column slab without a workspace
+        kq.set_option(kq.OPT_GEMV_TOKENS, 0)  # raises on failure
+        assert kq.get_option(kq.OPT_GEMV_TOKENS) == 0
+        try:
+            y2 = kq.q4_linear(wd, xd, out_dtype=kq.DTYPE_F32).cpu().numpy()
+        finally:
+            kq.set_option(kq.OPT_GEMV_TOKENS, 1)
+        assert np.max(np.abs(y - y2)) <= 1e-4 * rms(want)
+
+
+@pytest.mark.parametrize("m", [2, 3, 4])
+@pytest.mark.parametrize("n,k", [(500, 2048), (37, 1408), (11008, 2048)])
+def test_gemv_tokens_gate_up(kq, m, n, k):
+    s = synth()
+    case(f"gate_up tokens m={m} n={n} k={k}")
+    g, u = s.q4_weight(n, k, 80 + m), s.q4_weight(n, k, 90 + m)
+    x = s.bf16_normal((m, k), 100 + m)
+    want = O.q4_gate_up_act(O.Q4Planar(*g), O.Q4Planar(*u), x)
+    a = kq.gate_up_act(q4_dev(kq, g), q4_dev(kq, u), dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy()
+    assert_rms_close(a, want, what=f"gate_up m={m}")
+
+
 # ---------------------------------------------------------------- gate+up+act and MLP
 
 @pytest.mark.parametrize("name", ["swiglu_9x128", "swiglu_11x128"])
