@@ -87,6 +87,8 @@ const char *kr_last_error(void);
 #define KR_OPT_GEMV_TOKENS 9            /* 2 <= m <= 4: 1 (default) the GEMV kernels take all tokens per
                                            unpacked word (k <= 2048, or k <= 16384 without gate/up);
                                            0 the few-token MFMA kernel */
+#define KR_OPT_MOE_GEMV 10              /* kr_q4_moe_experts with tokens * topk <= 16: 1 (default) one GEMV
+                                           per (expert, token) pair, 0 the grouped MFMA kernel */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 

@@ -232,6 +232,10 @@ int kr_set_option(int option, int value) {
             if (value != 0 && value != 1) return fail(KR_E_INVALID, "gemv tokens must be 0 or 1");
             tuning().gemv_tokens = value;
             return ok();
+        case KR_OPT_MOE_GEMV:
+            if (value != 0 && value != 1) return fail(KR_E_INVALID, "moe gemv must be 0 or 1");
+            tuning().moe_gemv = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -247,6 +251,7 @@ int kr_get_option(int option) {
         case KR_OPT_PREFILL_KERNEL: return tuning().prefill_kernel;
         case KR_OPT_GEMV_LONG_ROWS: return tuning().gemv_long_rows;
         case KR_OPT_GEMV_TOKENS: return tuning().gemv_tokens;
+        case KR_OPT_MOE_GEMV: return tuning().moe_gemv;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -516,6 +521,38 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
     const uint32_t assign = tokens * topk;
     uint16_t *h = (uint16_t *)workspace;                                              // [assign, inter] bf16, sorted order
     float *d = (float *)((char *)workspace + round_up((size_t)assign * inter * 2, 256));  // [assign, hidden] f32
+
+    if (tuning().moe_gemv && assign <= kMoeGemvMaxAssign && moe_gemv_fits(hidden) && moe_gemv_fits(inter)) {
+        // few assignments: one m = 1 GEMV per (expert, token) pair, every expert row read once per assignment
+        MoeGemvArgs g{};
+        g.w = to_mat(gate);
+        g.w2 = to_mat(up);
+        g.rows = inter;
+        g.x = x;
+        g.x_div = topk;  // X row of an assignment = its token
+        g.offsets = offsets;
+        g.sorted = sorted_assign;
+        g.experts = experts;
+        g.assign = assign;
+        g.out = h;
+        g.ldo = inter;
+        g.act = activation;
+        if (hipError_t e = launch_moe_gemv(g, kGateUpBF16, s)) return hip_status(e, "kr_q4_moe_experts (gate/up)");
+        MoeGemvArgs dn{};
+        dn.w = dn.w2 = to_mat(down);
+        dn.rows = hidden;
+        dn.x = h;
+        dn.offsets = offsets;
+        dn.sorted = sorted_assign;
+        dn.experts = experts;
+        dn.assign = assign;
+        dn.out = d;
+        dn.ldo = hidden;
+        dn.out_scatter = 1;  // result rows back in assignment order
+        if (hipError_t e = launch_moe_gemv(dn, kStoreF32, s)) return hip_status(e, "kr_q4_moe_experts (down)");
+        return hip_status(launch_moe_combine(d, weights, tokens, topk, hidden, y, y_dtype == KR_DTYPE_F32, accumulate, s),
+                          "kr_q4_moe_experts (combine)");
+    }
 
     SkinnyArgs g{};
     g.w = to_mat(gate);

@@ -36,6 +36,7 @@ struct Tuning {
                                        // 0 = split-K block kernel
     int gemv_tokens = 1;               // 2 <= m <= 4: GEMV kernels over the tokens (1) or the few-token
                                        // MFMA kernel (0)
+    int moe_gemv = 1;                  // MoE with <= 16 assignments: routed GEMV (1) or grouped MFMA kernel (0)
 };
 Tuning &tuning();
 
@@ -107,6 +108,28 @@ struct SkinnyArgs {
     uint32_t max_active;      // upper bound of non-empty buckets (sizes the grid)
 };
 hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s);
+
+// Routed MoE GEMV: one token per (expert, sorted position) pair on the m = 1
+// wave kernel, for few assignments.  Position p of the expert-sorted list
+// belongs to the expert whose bucket [offsets[e], offsets[e+1]) holds it; its
+// x row is sorted[p] / x_div (x_div > 0) or p, its output row sorted[p]
+// (out_scatter) or p.  k <= 2048.
+struct MoeGemvArgs {
+    Q4Mat w, w2;                // stacked experts (w2: up matrix of the gate/up epilogue, else == w)
+    uint32_t rows;              // rows per expert
+    const uint16_t *x;          // bf16 [.., k]
+    uint32_t x_div;
+    const uint32_t *offsets;    // [experts + 1]
+    const uint32_t *sorted;     // [assign]
+    uint32_t experts, assign;
+    void *out;                  // [.., ldo]
+    uint32_t ldo;
+    int out_scatter, act;
+    uint32_t tiles_per;         // set by the launcher
+};
+constexpr uint32_t kMoeGemvMaxAssign = 16;  // the routed GEMV is used up to this many assignments
+bool moe_gemv_fits(uint32_t k);
+hipError_t launch_moe_gemv(MoeGemvArgs &a, int epilogue, hipStream_t s);
 
 // ---- MoE routing and combine (moe.hip)
 constexpr uint32_t kRouteMaxTopK = 16;      // top-k list length of the routing kernel

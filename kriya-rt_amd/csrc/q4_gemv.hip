@@ -319,6 +319,123 @@ static hipError_t launch_batch_epi(GemvBatch &gb, const uint16_t *x, hipStream_t
 
 bool gemv_batch_supported(uint32_t k) { return k % 64 == 0 && k <= 2 * 64 * 32; }
 
+// ---------------------------------------------------------------- routed MoE GEMV
+
+// Items are (sorted position p, row tile) pairs, p-major; wave w takes the
+// contiguous run [w * per, (w + 1) * per), so that its items mostly share one
+// position: the expert lookup and the x pairs are redone only when p changes.
+// Expert of p: the number of bucket ends offsets[1..E] <= p (one ballot per 64
+// experts).  The next item's words are requested before the current item is
+// reduced and stored, as in the wave kernel.
+template <int EPI>
+__global__ __launch_bounds__(256) void q4_moe_gemv_kernel(MoeGemvArgs a) {
+    constexpr int R = 2;
+    constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t nwaves = gridDim.x * 4;
+    const uint32_t total = a.assign * a.tiles_per;
+    const uint32_t per = (total + nwaves - 1) / nwaves;
+    const uint32_t t_begin = wave * per, t_end = min(t_begin + per, total);
+    if (t_begin >= t_end) return;
+    const uint32_t K = a.w.k, nchunks = K >> 5, wpr = K >> 3, groups = K >> 6;
+    const uint32_t kMask = sgpr_const(0x000F000Fu);
+    const uint32_t kMagic = vgpr_const(0x43004300u);
+    const uint32_t kSelLo = sgpr_const(0x05040100u);
+    const uint32_t kSelHi = sgpr_const(0x07060302u);
+    const bool live = (uint32_t)lane < nchunks;
+    const uint32_t c = live ? (uint32_t)lane : 0u;
+
+    auto expert_of = [&](uint32_t p) -> uint32_t {
+        uint32_t e = 0;
+        for (uint32_t j0 = 0; j0 < a.experts; j0 += kWave) {
+            const uint32_t j = j0 + (uint32_t)lane;
+            const bool le = j < a.experts && a.offsets[j + 1] <= p;
+            e += (uint32_t)__popcll(__ballot(le));
+        }
+        return e;
+    };
+    // per-position state: views of the expert's matrices, the x pairs, the output row base
+    Q4Mat A = a.w, B = a.w2;
+    GemvOut o{nullptr, nullptr, a.act, 0};
+    XChunk xc;
+    uint32_t cur_p = 0xFFFFFFFFu;
+    auto enter = [&](uint32_t p) {
+        const uint32_t e = expert_of(p);
+        const size_t r0 = (size_t)e * a.rows;
+        A.qw = a.w.qw + r0 * wpr;
+        A.sc = a.w.sc + r0 * groups;
+        A.bi = a.w.bi + r0 * groups;
+        B.qw = a.w2.qw + r0 * wpr;
+        B.sc = a.w2.sc + r0 * groups;
+        B.bi = a.w2.bi + r0 * groups;
+        A.n = B.n = a.rows;
+        const uint32_t sp = a.sorted[p];
+        const uint32_t xr = a.x_div ? sp / a.x_div : p;
+        const uint32_t orow = a.out_scatter ? sp : p;
+        const size_t esz = (EPI == kStoreF32 || EPI == kAccF32 || EPI == kGateUpF32) ? 4 : 2;
+        o.out = reinterpret_cast<char *>(a.out) + (size_t)orow * a.ldo * esz;
+        load_xchunk(xc, a.x + (size_t)xr * K, c, kSelLo, kSelHi);
+        cur_p = p;
+    };
+
+    const u32x4 *rq[R];
+    const uint16_t *rs[R];
+    const uint16_t *rb[R];
+    u32x4 wv[R];
+    uint32_t sv[R], bv[R];
+    auto fetch = [&](uint32_t lt) {
+        tile_rows<R, kGateUp>(A, B, lt, rq, rs, rb);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            wv[r] = ld_stream(rq[r] + c);
+            sv[r] = ld_stream(rs[r] + (c >> 1));
+            bv[r] = ld_stream(rb[r] + (c >> 1));
+        }
+    };
+    uint32_t t = t_begin;
+    enter(t / a.tiles_per);
+    fetch(t % a.tiles_per);
+    for (;;) {
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float d = chunk_dot(wv[r], sv[r], bv[r], xc, 0.0f, kMask, kMagic);
+            acc[r] = live ? d : 0.0f;
+        }
+        const uint32_t lt = t % a.tiles_per;
+        const GemvOut oc = o;
+        const uint32_t tn = t + 1;
+        if (tn < t_end) {
+            const uint32_t pn = tn / a.tiles_per;
+            if (pn != cur_p) enter(pn);
+            fetch(tn % a.tiles_per);
+        }
+        const float tot = wave_reduce_rows<R>(acc, lane);
+        tile_epilogue<R, EPI>(tot, lane, lt, a.rows, oc, 0.0f);
+        if (tn >= t_end) break;
+        t = tn;
+    }
+}
+
+bool moe_gemv_fits(uint32_t k) { return k % 64 == 0 && k <= 2048; }
+
+hipError_t launch_moe_gemv(MoeGemvArgs &a, int epilogue, hipStream_t s) {
+    if (!moe_gemv_fits(a.w.k) || a.assign == 0) return hipErrorInvalidValue;
+    const bool gate_up = epilogue == kGateUpBF16 || epilogue == kGateUpF32;
+    a.tiles_per = gate_up ? a.rows : (a.rows + 1) / 2;  // two rows per tile: (gate, up) or a row pair
+    const uint32_t total = a.assign * a.tiles_per;
+    const uint32_t blocks = cap_blocks((total + 3) / 4, (uint32_t)tuning().gemv_persistent_blocks);
+    switch (epilogue) {
+        case kGateUpBF16:
+            hipLaunchKernelGGL((q4_moe_gemv_kernel<kGateUpBF16>), dim3(blocks), dim3(256), 0, s, a);
+            break;
+        case kStoreF32: hipLaunchKernelGGL((q4_moe_gemv_kernel<kStoreF32>), dim3(blocks), dim3(256), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- 2 <= m <= 4 tokens
 
 template <int EPI, int M>

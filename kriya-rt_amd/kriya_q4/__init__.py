@@ -31,6 +31,7 @@ OPT_GEMV_ROWS_PER_WAVE, OPT_GEMV_MAX_BLOCKS, OPT_GEMV_SPLIT_K_CHUNKS = 1, 2, 3
 OPT_GEMV_BLOCK_ROWS, OPT_GEMV_PERSISTENT_BLOCKS, OPT_SKINNY_MAX_BLOCKS, OPT_PREFILL_KERNEL = 4, 5, 6, 7
 OPT_GEMV_LONG_ROWS = 8
 OPT_GEMV_TOKENS = 9
+OPT_MOE_GEMV = 10
 
 _lib = None
 

@@ -149,6 +149,29 @@ def test_moe_experts_small(kq, T, E, K, hidden, inter):
     assert_bf16_rounded_close(host_bits(res), O.bf16_to_f32(r0) + want, rms(want), rel=1e-2, what="moe acc")
 
 
+@pytest.mark.parametrize("T,E,K,hidden,inter", [(4, 3, 2, 256, 128), (2, 60, 4, 2048, 1408), (16, 8, 1, 512, 384),
+                                                (1, 60, 4, 2048, 1408)])
+def test_moe_routed_gemv_and_grouped_paths(kq, T, E, K, hidden, inter):
+    """Few assignments (T * K <= 16) run one GEMV per (expert, token) pair; the grouped MFMA kernel
+    (KR_OPT_MOE_GEMV = 0) must give the same result to the RMS bar, both against the oracle."""
+    case(f"moe routed gemv vs grouped T={T} E={E} K={K} hidden={hidden} inter={inter}")
+    g, u, d, x, logits, route, want = moe_case(kq, T, E, K, hidden, inter, 4500 + T + E)
+    r = route_from_oracle(kq, *route, T, E, K)
+    gd, ud, dd = q4_dev(kq, g), q4_dev(kq, u), q4_dev(kq, d)
+    y = kq.moe_experts(gd, ud, dd, E, dev_bf16(x), r).cpu().numpy()
+    assert_rms_close(y, want, what="routed gemv")
+    kq.set_option(kq.OPT_MOE_GEMV, 0)
+    try:
+        y2 = kq.moe_experts(gd, ud, dd, E, dev_bf16(x), r).cpu().numpy()
+    finally:
+        kq.set_option(kq.OPT_MOE_GEMV, 1)
+    assert_rms_close(y2, want, what="grouped")
+    r0 = synth().bf16_normal((T, hidden), 4599)
+    res = dev_bf16(r0).clone()
+    kq.moe_experts(gd, ud, dd, E, dev_bf16(x), r, y=res, accumulate=True)
+    assert_bf16_rounded_close(host_bits(res), O.bf16_to_f32(r0) + want, rms(want), rel=1e-2, what="routed acc")
+
+
 @pytest.mark.parametrize("T", [1, 64])
 def test_moe_config4(kq, T):
     """Config 4: 60 experts, top-4, hidden 2048, expert intermediate 1408, device routing."""
