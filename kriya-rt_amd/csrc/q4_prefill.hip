@@ -37,6 +37,8 @@
 // Block ids are remapped so that the M tiles of one N tile run on one XCD and
 // share its L2; split-K (grid.y) writes f32 partials that
 // q4_mfma_splitk_reduce_kernel sums in split order.
+#include <type_traits>
+
 #include "kr_internal.hpp"
 
 
@@ -107,11 +109,15 @@ struct PrefillTile {
     static constexpr int kWaveRows = kFPM * 16;         // output columns per wave
     static constexpr int kBN = WAVES * kWaveRows;       // output columns per block
     static constexpr int kBufBytes = kBM * 128;         // one 64-column X slice in fp16
-    static constexpr int kLdsBytes = 2 * kBufBytes;
     static_assert(NF % NW == 0, "gate/up needs pairs of fragments");
 };
 
-template <int MF, int NF, int WAVES, int NW, int OCC, int EPI>
+// D: steps of look-ahead.  The X slice and the weights of step g + D are
+// requested at step g (ring of D + 1 X buffers and weight register sets).
+// vmcnt completes in issue order, so waiting for the X slice of step g + 1 at
+// the end of step g also waits for every load issued before it: with X and
+// weights requested together D steps ahead, both get D steps of latency.
+template <int MF, int NF, int WAVES, int NW, int OCC, int EPI, int D>
 __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs args) {
     using T = PrefillTile<MF, NF, WAVES, NW>;
     constexpr int FPM = T::kFPM;
@@ -236,36 +242,55 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
     };
 
     if (g_begin < g_end) {
-        WRegs w0, w1;
-        dma_x(g_begin, 0);
-        load_w(g_begin, w0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        constexpr int NB = D + 1;
+        constexpr int kWLoads = 3 * NF;
+        // loads issued after the X slice of a step: its weights and the later D - 1 (X, weights) pairs
+        constexpr int kAfterX = kWLoads + (D - 1) * (XI + kWLoads);
+        WRegs w[NB];
+        // Requests past the last group are clamped to group G - 1 (in bounds, never used), so
+        // that every step issues the same loads and the waits are fixed counts.
+        auto gc = [&](uint32_t g) { return min(g, G - 1); };
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            dma_x(gc(g_begin + d), d);
+            __builtin_amdgcn_sched_barrier(0);  // X before the weights (vmcnt order)
+            load_w(gc(g_begin + d), w[d]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfterX) : "memory");
         convert_x(0);
         __syncthreads();
-        // Loads of the next step are issued unconditionally (the group index is
-        // clamped, so offsets stay inside the buffers): no branch sits between
-        // a load and its use.  X of step g+1 lands in the other buffer while
-        // step g computes; vmcnt counts in issue order, so waiting until only
-        // the weight loads issued after it are outstanding covers the DMA.
-        uint32_t g = g_begin;
-        int buf = 0;
-        constexpr int kWLoads = 3 * NF;
-        auto step = [&](uint32_t gn, WRegs &cur, WRegs &next) {
-            dma_x(gn, buf ^ 1);
-            __builtin_amdgcn_sched_barrier(0);  // the DMA is issued before the weight loads (vmcnt order)
-            load_w(gn, next);
+        auto step = [&](auto I, uint32_t g) {
+            constexpr int i = decltype(I)::value;
+            constexpr int pf = (i + D) % NB;
+            dma_x(gc(g + D), pf);
+            __builtin_amdgcn_sched_barrier(0);
+            load_w(gc(g + D), w[pf]);
             __builtin_amdgcn_sched_barrier(0);  // keep the loads at the top of the step
-            compute(buf, cur);
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kWLoads) : "memory");
-            convert_x(buf ^ 1);
+            compute(i, w[i]);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfterX) : "memory");  // X slice of step g + 1
+            convert_x((i + 1) % NB);
             __syncthreads();
-            buf ^= 1;
         };
-        for (; g + 2 <= g_end; g += 2) {
-            step(min(g + 1, G - 1), w0, w1);
-            step(min(g + 2, G - 1), w1, w0);
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
+        using S3 = std::integral_constant<int, 3>;
+        static_assert(NB >= 2 && NB <= 4, "look-ahead of 1 to 3 steps");
+        uint32_t g = g_begin;
+        for (; g + NB <= g_end; g += NB) {
+            step(S0{}, g);
+            step(S1{}, g + 1);
+            if constexpr (NB > 2) step(S2{}, g + 2);
+            if constexpr (NB > 3) step(S3{}, g + 3);
         }
-        if (g < g_end) compute(buf, w0);
+        if (g < g_end) step(S0{}, g);
+        if constexpr (NB > 2) {
+            if (g + 1 < g_end) step(S1{}, g + 1);
+        }
+        if constexpr (NB > 3) {
+            if (g + 2 < g_end) step(S2{}, g + 2);
+        }
     }
 
     // ---- epilogue: lane holds C[4 * kq + v][c] of each 16 x 16 fragment
@@ -302,9 +327,10 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
     }
 }
 
-template <int MF, int NF, int WAVES, int NW, int OCC>
+template <int MF, int NF, int WAVES, int NW, int OCC, int D>
 static hipError_t launch_prefill_shape(MfmaArgs &a, hipStream_t s) {
     using T = PrefillTile<MF, NF, WAVES, NW>;
+    constexpr int kLds = (D + 1) * T::kBufBytes;
     uint32_t tiles = 0;
     const uint32_t tiles_m = (a.m + T::kBM - 1) / T::kBM;
     for (int i = 0; i < a.np; ++i) {
@@ -313,23 +339,26 @@ static hipError_t launch_prefill_shape(MfmaArgs &a, hipStream_t s) {
     }
     const dim3 grid(tiles, a.ksplit);
     if (a.ksplit > 1) {
-        hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaPartial>), grid, dim3(T::kThreads),
-                           T::kLdsBytes, s, a);
+        hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaPartial, D>), grid, dim3(T::kThreads),
+                           kLds, s, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         return launch_splitk_reduce(a, NW, s);
     }
-    hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaDirect>), grid, dim3(T::kThreads), T::kLdsBytes,
-                       s, a);
+    hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaDirect, D>), grid, dim3(T::kThreads), kLds, s,
+                       a);
     return hipGetLastError();
 }
 
-// Launch shapes (measured on MI355X at M = 512, K = 2048 / 11008):
-//   gate/up: 128 token rows x (4 waves x 16 gate + 16 up rows), 3 waves per SIMD;
-//   plain:    96 token rows x (4 waves x 32 rows), 4 waves per SIMD -- the
-//             N = 2048 projections need the extra blocks more than the reuse.
+// Launch shapes (measured on MI355X at M = 512, K = 2048 / 11008), two steps
+// of look-ahead:
+//   gate/up: 128 token rows x (4 waves x 16 gate + 16 up rows), 3 waves per
+//            SIMD (wider or narrower tiles measured slower: 105-160 us vs 97-100 us);
+//   plain:    64 token rows x (4 waves x 16 rows), 4 waves per SIMD.  The
+//             N = 2048 projections are short of blocks with larger tiles
+//             (96 x 128: down 145 us, o 33 us; 64 x 64: down 72 us, o 17.6 us).
 using GateUpShape = PrefillTile<8, 2, 4, 2>;
-using PlainShape = PrefillTile<6, 2, 4, 1>;
+using PlainShape = PrefillTile<4, 1, 4, 1>;
 
 uint32_t prefill_block_m(bool gate_up) { return gate_up ? GateUpShape::kBM : PlainShape::kBM; }
 uint32_t prefill_block_rows(bool gate_up) { return gate_up ? GateUpShape::kBN : PlainShape::kBN; }
@@ -346,9 +375,8 @@ bool prefill_supported(const MfmaArgs &a) {
 }
 
 hipError_t launch_prefill(MfmaArgs &a, hipStream_t s) {
-    const bool gate_up = a.p[0].w2.qw != nullptr;
-    if (gate_up) return launch_prefill_shape<8, 2, 4, 2, 3>(a, s);
-    return launch_prefill_shape<6, 2, 4, 1, 4>(a, s);
+    if (a.p[0].w2.qw != nullptr) return launch_prefill_shape<8, 2, 4, 2, 3, 2>(a, s);
+    return launch_prefill_shape<4, 1, 4, 1, 4, 2>(a, s);
 }
 
 }  // namespace kr
