@@ -202,9 +202,39 @@ __global__ __launch_bounds__(1024) void moe_route_kernel(const float *logits, ui
     }
 }
 
+// Softmax and top-k only, one token per wave and 16 tokens per block, for
+// token counts where one block would route them in several serial rounds.
+__global__ __launch_bounds__(1024) void moe_topk_kernel(const float *logits, uint32_t T, uint32_t E, uint32_t K,
+                                                        int normalize, uint32_t *experts, float *weights) {
+    __shared__ uint32_t s_ti[16][kRouteMaxTopK];
+    __shared__ float s_tv[16][kRouteMaxTopK];
+    __shared__ __attribute__((aligned(16))) float s_pr[16][kMaxExperts];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.x * 16 + wave;
+    if (t >= T) return;
+    float lv[kRoutePer];
+    load_logits(logits + (size_t)t * E, E, lane, lv);
+    route_token_wave(lv, E, K, normalize, lane, s_pr[wave], s_ti[wave], s_tv[wave]);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < K) {
+        experts[t * K + lane] = s_ti[wave][lane];
+        weights[t * K + lane] = s_tv[wave][lane];
+    }
+}
+
 hipError_t launch_moe_route(const float *logits, uint32_t T, uint32_t E, uint32_t K, int normalize,
                             uint32_t *experts, float *weights, uint32_t *counts, uint32_t *offsets, uint32_t *sorted,
                             hipStream_t s) {
+    if (logits && T > 16) {
+        // more tokens than one block routes in a round: top-k on ceil(T / 16) blocks, then the
+        // counts, offsets and sorted list from the chosen experts (the same results)
+        hipLaunchKernelGGL(moe_topk_kernel, dim3((T + 15) / 16), dim3(1024), 0, s, logits, T, E, K, normalize, experts,
+                           weights);
+        if (hipError_t e = hipGetLastError()) return e;
+        logits = nullptr;
+    }
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), 0, s, logits, T, E, K, normalize, experts, weights,
                        counts, offsets, sorted);
     return hipGetLastError();
