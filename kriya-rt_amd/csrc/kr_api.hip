@@ -115,8 +115,10 @@ MfmaProblem problem(const Q4Mat &w, const Q4Mat *w2, void *out, const uint16_t *
 // another path (returns hipErrorInvalidValue).
 hipError_t run_skinny(const Q4Mat &w, const Q4Mat *w2, const uint16_t *x, uint32_t m, void *out,
                       const uint16_t *bias, uint32_t ldo, int out_dtype, int accumulate, int act, float *partial,
-                      hipStream_t s) {
+                      hipStream_t s, const uint16_t *ln_w = nullptr, float eps = 0.0f) {
     SkinnyArgs a{};
+    a.ln_w = ln_w;
+    a.eps = eps;
     a.w = w;
     if (w2) a.w2 = *w2;
     a.x = x;
@@ -149,6 +151,27 @@ hipError_t run_skinny(const Q4Mat &w, const Q4Mat *w2, const uint16_t *x, uint32
     r.partial = partial;
     r.ksplit = ks;
     return launch_splitk_reduce(r, w2 ? 2 : 1, s);
+}
+
+// Q, K and V in one few-token launch (k within one slab), x optionally RMS-normalised while staged.
+hipError_t run_skinny_qkv(const kr_q4_matrix *const *mats, const uint16_t *const *biases, void *const *outs,
+                          const uint16_t *x, uint32_t m, int out_dtype, const uint16_t *ln_w, float eps,
+                          hipStream_t s) {
+    SkinnyArgs a{};
+    a.w = to_mat(mats[0]);
+    a.x = x;
+    a.m = m;
+    a.k = mats[0]->k;
+    a.ldx = mats[0]->k;
+    a.out = outs[0];
+    a.bias = biases[0];
+    a.ldo = mats[0]->n;
+    a.out_f32 = out_dtype == KR_DTYPE_F32;
+    for (int i = 0; i < 2; ++i) a.more[i] = SkinnyArgs::More{to_mat(mats[i + 1]), outs[i + 1], biases[i + 1], mats[i + 1]->n};
+    a.nmore = 2;
+    a.ln_w = ln_w;
+    a.eps = eps;
+    return launch_skinny(a, s);
 }
 
 bool skinny_fits(uint32_t m, const Q4Mat &w, bool have_partial) {
@@ -383,14 +406,8 @@ int kr_q4_qkv(const kr_q4_matrix *q, const kr_q4_matrix *k, const kr_q4_matrix *
         }
         return ok();
     }
-    if (skinny_fits(m, to_mat(q), false) && skinny_supported(to_mat(k)) && skinny_supported(to_mat(v))) {
-        for (int i = 0; i < 3; ++i) {
-            const hipError_t e = run_skinny(to_mat(mats[i]), nullptr, x, m, outs[i], biases[i], mats[i]->n, out_dtype,
-                                            0, 0, nullptr, s);
-            if (e != hipSuccess) return hip_status(e, "kr_q4_qkv");
-        }
-        return ok();
-    }
+    if (skinny_fits(m, to_mat(q), false) && skinny_supported(to_mat(k)) && skinny_supported(to_mat(v)))
+        return hip_status(run_skinny_qkv(mats, biases, outs, x, m, out_dtype, nullptr, 0.0f, s), "kr_q4_qkv");
     MfmaArgs args = mfma_args(x, m, q->k, out_dtype, 0);
     for (int i = 0; i < 3; ++i) args.p[i] = problem(to_mat(mats[i]), nullptr, outs[i], biases[i], mats[i]->n);
     args.np = 3;
@@ -401,6 +418,27 @@ size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermedi
     size_t bytes = round_up((size_t)m * intermediate * 2, 256);
     if (m > 1) bytes += partial_bytes(m, hidden, intermediate, 1);  // split-K partials of the down projection
     return bytes;
+}
+
+// The MLP's down projection, accumulated into h, after the activation `act` (bf16 [m, inter]) was
+// written to the start of `workspace` (kr_q4_mlp_workspace_bytes layout: act, then split-K partials).
+static int mlp_down(const kr_q4_matrix *gate, const kr_q4_matrix *down, const uint16_t *act, void *h, int h_dtype,
+                    uint32_t m, void *workspace, void *stream) {
+    if (m == 1 || (tuning().gemv_tokens && gemv_tokens_supported(m, gate->k, true) &&
+                   gemv_tokens_supported(m, down->k, false)))
+        return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
+    // down projection: few N tiles at small m, so K is split over blocks; partials live in the workspace
+    float *partial = (float *)((char *)workspace + round_up((size_t)m * gate->n * 2, 256));
+    if (skinny_fits(m, to_mat(down), true))
+        return hip_status(run_skinny(to_mat(down), nullptr, act, m, h, nullptr, down->n, h_dtype, 1, 0, partial,
+                                     (hipStream_t)stream),
+                          "kr_q4_mlp (down)");
+    MfmaArgs args = mfma_args(act, m, down->k, h_dtype, 1);
+    args.p[0] = problem(to_mat(down), nullptr, h, nullptr, down->n);
+    args.np = 1;
+    const int bm = bm_class(m);
+    choose_split_k(args, bm, partial);
+    return hip_status(launch_mfma(args, bm, (hipStream_t)stream), "kr_q4_mlp (down)");
 }
 
 int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, const uint16_t *x,
@@ -428,21 +466,7 @@ int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matr
     if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
     uint16_t *act = (uint16_t *)workspace;
     if (int rc = kr_q4_gate_up_act(gate, up, x, m, act, KR_DTYPE_BF16, activation, stream)) return rc;
-    if (m == 1 || (tuning().gemv_tokens && gemv_tokens_supported(m, gate->k, true) &&
-                   gemv_tokens_supported(m, down->k, false)))
-        return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
-    // down projection: few N tiles at small m, so K is split over blocks; partials live in the workspace
-    float *partial = (float *)((char *)workspace + round_up((size_t)m * gate->n * 2, 256));
-    if (skinny_fits(m, to_mat(down), true))
-        return hip_status(run_skinny(to_mat(down), nullptr, act, m, h, nullptr, down->n, h_dtype, 1, 0, partial,
-                                     (hipStream_t)stream),
-                          "kr_q4_mlp (down)");
-    MfmaArgs args = mfma_args(act, m, down->k, h_dtype, 1);
-    args.p[0] = problem(to_mat(down), nullptr, h, nullptr, down->n);
-    args.np = 1;
-    const int bm = bm_class(m);
-    choose_split_k(args, bm, partial);
-    return hip_status(launch_mfma(args, bm, (hipStream_t)stream), "kr_q4_mlp (down)");
+    return mlp_down(gate, down, act, h, h_dtype, m, workspace, stream);
 }
 
 int kr_moe_route(const float *logits, uint32_t tokens, uint32_t experts, uint32_t topk, int normalize,
@@ -668,6 +692,13 @@ int kr_rmsnorm_q4_qkv(const uint16_t *h, const uint16_t *ln_weight, float eps, c
         return hip_status(launch_gemv_batch(ms, nullptr, h, outs, biases, 3, epi, 0, ln_weight, eps, s),
                           "kr_rmsnorm_q4_qkv");
     }
+    if (skinny_fits(m, to_mat(q), false) && skinny_supported(to_mat(k)) && skinny_supported(to_mat(v))) {
+        // few tokens: the norm is applied while the few-token kernel stages x (xnorm is not written)
+        const kr_q4_matrix *mats[3] = {q, k, v};
+        const uint16_t *biases[3] = {q_bias, k_bias, v_bias};
+        void *outs[3] = {q_out, k_out, v_out};
+        return hip_status(run_skinny_qkv(mats, biases, outs, h, m, out_dtype, ln_weight, eps, s), "kr_rmsnorm_q4_qkv");
+    }
     if (!xnorm || !aligned(xnorm, 16)) return fail(KR_E_INVALID, "xnorm (16-byte aligned) is required for m > 1");
     if (int rc = hip_status(launch_rmsnorm(h, ln_weight, m, q->k, eps, xnorm, s), "kr_rmsnorm_q4_qkv")) return rc;
     return kr_q4_qkv(q, k, v, q_bias, k_bias, v_bias, xnorm, m, q_out, k_out, v_out, out_dtype, stream);
@@ -706,6 +737,17 @@ int kr_rmsnorm_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
                                 "kr_rmsnorm_q4_mlp"))
             return rc;
         return kr_q4_linear(down, act, 1, h, KR_DTYPE_BF16, 1, stream);
+    }
+    const bool tokens = tuning().gemv_tokens && gemv_tokens_supported(m, gate->k, true);
+    if (!tokens && skinny_fits(m, to_mat(gate), false) && skinny_supported(to_mat(up))) {
+        // few tokens on the matrix cores: the norm is applied while gate/up stages x
+        uint16_t *act = (uint16_t *)workspace;
+        const Q4Mat g = to_mat(gate), u = to_mat(up);
+        if (int rc = hip_status(run_skinny(g, &u, h, m, act, nullptr, gate->n, KR_DTYPE_BF16, 0, activation, nullptr, s,
+                                           ln_weight, eps),
+                                "kr_rmsnorm_q4_mlp"))
+            return rc;
+        return mlp_down(gate, down, act, h, KR_DTYPE_BF16, m, workspace, stream);
     }
     uint16_t *xnorm = (uint16_t *)((char *)workspace + mlp_bytes);
     if (int rc = hip_status(launch_rmsnorm(h, ln_weight, m, gate->k, eps, xnorm, s), "kr_rmsnorm_q4_mlp")) return rc;

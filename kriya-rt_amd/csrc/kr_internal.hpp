@@ -106,6 +106,20 @@ struct SkinnyArgs {
     uint32_t x_div;           // > 0: X row of sorted position p is sorted[p] / x_div; 0: row p
     int out_scatter;          // 1: result row of sorted position p goes to row sorted[p]; 0: row p
     uint32_t max_active;      // upper bound of non-empty buckets (sizes the grid)
+    // dense mode only: up to two more problems sharing x and k (the K and V
+    // projections next to Q), each with its own weights, output and bias
+    struct More {
+        Q4Mat w;
+        void *out;
+        const uint16_t *bias;
+        uint32_t ldo;
+    } more[2];
+    int nmore;
+    uint32_t tile_begin[4];   // set by the launcher: problem i's first tile; [nmore + 1] = all tiles
+    // dense mode, k <= 2048: x rows are RMS-normalised while staged,
+    // bf16(x * rsqrt(mean(x^2) + eps) * ln_w) as kr_rmsnorm computes it
+    const uint16_t *ln_w;
+    float eps;
 };
 hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s);
 

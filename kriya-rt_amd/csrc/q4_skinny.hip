@@ -181,20 +181,24 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         }
     };
 
-    // ---- this block's contiguous run of work items (active expert, tile)
+    // ---- this block's contiguous run of work items (active expert, tile); dense mode: the
+    // tiles of the problems one after the other
     const uint32_t tiles_per_expert = (a.expert_rows + kTileRows - 1) / kTileRows;
-    const uint32_t total = nactive * tiles_per_expert;
+    const uint32_t total = kGrouped ? nactive * tiles_per_expert : a.tile_begin[a.nmore + 1];
     const uint32_t nblk = gridDim.x / a.ksplit;
     const uint32_t per = (total + nblk - 1) / nblk;
     const uint32_t run_begin = (blockIdx.x / a.ksplit) * per;
     const uint32_t run_end = min(run_begin + per, total);
     if (run_begin >= run_end) return;
 
-    // weight rows: lanes 0-7 gate, 8-15 up (gate/up tiles); lane r16 otherwise
+    // The current problem (dense mode: one of up to three sharing x; its fields
+    // are selected by value, uniform).  Weight rows: lanes 0-7 gate, 8-15 up
+    // (gate/up tiles); lane r16 otherwise.
+    Q4Mat cw = a.w, cw2 = a.w2;
+    void *cout = a.out;
+    const uint16_t *cbias = a.bias;
+    uint32_t cldo = a.ldo, crows = a.expert_rows;
     const bool up_lane = kGateUp && r16 >= 8;
-    const uint32_t *qw_base = up_lane ? a.w2.qw : a.w.qw;
-    const uint16_t *sc_base = up_lane ? a.w2.sc : a.w.sc;
-    const uint16_t *bi_base = up_lane ? a.w2.bi : a.w.bi;
     const uint32_t kw = K >> 3, kg = K >> 6;
 
     // Tile words, double buffered (the buffer index is a compile-time
@@ -215,9 +219,12 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     bool eout = false;                                                      // it stores an output
     auto fetch = [&](auto BUF, uint32_t e, uint32_t t) {
         constexpr int b = decltype(BUF)::value;
+        const uint32_t *qw_base = up_lane ? cw2.qw : cw.qw;
+        const uint16_t *sc_base = up_lane ? cw2.sc : cw.sc;
+        const uint16_t *bi_base = up_lane ? cw2.bi : cw.bi;
         uint32_t f = kGateUp ? t * 8 + (r16 & 7) : t * 16 + r16;
-        f = f < a.expert_rows ? f : a.expert_rows - 1;  // tail rows re-read a valid row and are never stored
-        const size_t row = (size_t)e * a.expert_rows + f;
+        f = f < crows ? f : crows - 1;  // tail rows re-read a valid row and are never stored
+        const size_t row = (size_t)e * crows + f;
         const u32x4 *src = reinterpret_cast<const u32x4 *>(qw_base + row * kw + (k0 >> 3));
         // bf16 pairs (groups 2p, 2p+1) of piece p; 4-byte aligned (kg even, scales 4-byte aligned)
         const uint32_t *s32 = reinterpret_cast<const uint32_t *>(sc_base + row * kg + (k0 >> 6));
@@ -233,13 +240,13 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         // Unconditional loads (threads without an operand read x[0]), so that
         // no branch makes the compiler wait for them before its join.
         const uint32_t ef = kGateUp ? t * 8 + (ecol & 7) : t * 16 + ecol;
-        const bool ok = eout && ef < a.expert_rows;
-        const uint16_t *bsrc = (a.bias && ok) ? a.bias + (size_t)e * a.expert_rows + ef : a.x;
+        const bool ok = eout && ef < crows;
+        const uint16_t *bsrc = (cbias && ok) ? cbias + (size_t)e * crows + ef : a.x;
         pre_b[b] = *bsrc;
         // old output: one aligned u32 (a bf16 output reads the pair holding it)
-        const size_t o = (size_t)orow * a.ldo + ef;
-        const uint32_t *osrc = a.out_f32 ? reinterpret_cast<const uint32_t *>(a.out) + o
-                                         : reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(a.out) +
+        const size_t o = (size_t)orow * cldo + ef;
+        const uint32_t *osrc = a.out_f32 ? reinterpret_cast<const uint32_t *>(cout) + o
+                                         : reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(cout) +
                                                                               (o & ~(size_t)1));
         pre_o[b] = *((a.accumulate && ok) ? osrc : reinterpret_cast<const uint32_t *>(a.x));
     };
@@ -274,6 +281,58 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         }
     };
 
+    // LDS-only barrier: the weight prefetch stays in flight across it (a
+    // barrier with a memory fence would wait for every outstanding load).
+    auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+    // RMSNorm of the staged rows (dense mode, the whole row in this slab):
+    // every unit of a thread is column block u = tid % kUnits of rows
+    // tid / kUnits + 2 s, so one ln_w unit serves all of them.  Per-row sums of
+    // squares: wave sums, then the four waves of a row parity in order.
+    // (s_ss and s_scale live in the reduction buffer, unused until the first tile)
+    float (*s_ss)[4] = reinterpret_cast<float (*)[4]>(&red[0][0][0][0]);
+    float *s_scale = &red[1][0][0][0];
+    auto norm_x = [&](uint32_t rows) {
+        static_assert(NW * 64 == 2 * kUnits, "two rows per staging round");
+        const uint32_t u = (uint32_t)tid % kUnits, r0 = (uint32_t)tid / kUnits;
+        const bool ulive = u < npieces * 16;
+        const u32x4 wl = *reinterpret_cast<const u32x4 *>(a.ln_w + k0 + 8 * (ulive ? u : 0u));
+#pragma unroll
+        for (int st = 0; st < kStage; ++st) {
+            const uint32_t r = r0 + 2u * (uint32_t)st;
+            float ss = 0.0f;
+            if (ulive && r < rows) {
+                const uint32_t X[4] = {raw[st].x, raw[st].y, raw[st].z, raw[st].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float lo = __uint_as_float(X[i] << 16), hi = __uint_as_float(X[i] & 0xFFFF0000u);
+                    ss = fmaf(lo, lo, ss);
+                    ss = fmaf(hi, hi, ss);
+                }
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) s_ss[r][wave & 3] = ss;
+        }
+        lds_barrier();
+        if (tid < 16) {
+            const float tot = ((s_ss[tid][0] + s_ss[tid][1]) + s_ss[tid][2]) + s_ss[tid][3];
+            s_scale[tid] = 1.0f / sqrtf(tot / (float)K + a.eps);
+        }
+        lds_barrier();
+        const uint32_t W[4] = {wl.x, wl.y, wl.z, wl.w};
+#pragma unroll
+        for (int st = 0; st < kStage; ++st) {
+            const float scale = s_scale[r0 + 2u * (uint32_t)st];
+            uint32_t X[4] = {raw[st].x, raw[st].y, raw[st].z, raw[st].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float lo = __uint_as_float(X[i] << 16) * scale * __uint_as_float(W[i] << 16);
+                const float hi = __uint_as_float(X[i] & 0xFFFF0000u) * scale * __uint_as_float(W[i] & 0xFFFF0000u);
+                X[i] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+            }
+            raw[st] = u32x4{X[0], X[1], X[2], X[3]};
+        }
+    };
+
     // X fragment of slice (i, j) of this wave: unit 16 (p0 + i) + 4 g + j of row
     // r16, i.e. (swizzle) r16 * kUnits + 16 (p0 + i) + ((4 g + j) ^ r16): one
     // base per j, and i as an immediate offset.  The low 32 bits of a generic
@@ -300,9 +359,6 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         x[2] = __builtin_bit_cast(f16x8_t, v2);
         x[3] = __builtin_bit_cast(f16x8_t, v3);
     };
-    // LDS-only barrier: the weight prefetch stays in flight across it (a
-    // barrier with a memory fence would wait for every outstanding load).
-    auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
     // v_perm selector broadcasting this lane's half (group 2p + g/2) of a pair to both halves
     const uint32_t half_sel = (g >> 1) ? 0x03020302u : 0x01000100u;
@@ -334,15 +390,15 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         for (int v = 0; v < 4; ++v) red[par][wave][v][lane] = acc[v];
         lds_barrier();
         const uint32_t f = kGateUp ? t * 8 + (ecol & 7) : t * 16 + ecol;
-        if (eout && f < a.expert_rows) {
+        if (eout && f < crows) {
             const uint32_t L = 16u * (erow >> 2) + ecol, v = erow & 3u;
             float val = 0.0f;
 #pragma unroll
             for (int w = 0; w < NW; ++w) val += red[par][w][v][L];
             if (a.partial) {  // dense split-K: [ksplit, m, nw * n], gate at f, up at n + f
                 const uint32_t nw = kGateUp ? 2 : 1;
-                float *dst = a.partial + ((size_t)slab * a.m + erow) * (size_t)(nw * a.expert_rows);
-                dst[((kGateUp && ecol >= 8) ? a.expert_rows : 0u) + f] = val;
+                float *dst = a.partial + ((size_t)slab * a.m + erow) * (size_t)(nw * crows);
+                dst[((kGateUp && ecol >= 8) ? crows : 0u) + f] = val;
             } else {
                 if constexpr (kGateUp) {
                     float up = 0.0f;
@@ -350,13 +406,13 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
                     for (int w = 0; w < NW; ++w) up += red[par][w][v][L + 8];
                     val = activation(val, a.act) * up;
                 }
-                if (a.bias) val += bf16_to_f32(pre_b[b]);
-                const size_t o = (size_t)orow * a.ldo + f;
+                if (cbias) val += bf16_to_f32(pre_b[b]);
+                const size_t o = (size_t)orow * cldo + f;
                 if (a.out_f32) {
-                    reinterpret_cast<float *>(a.out)[o] = a.accumulate ? __uint_as_float(pre_o[b]) + val : val;
+                    reinterpret_cast<float *>(cout)[o] = a.accumulate ? __uint_as_float(pre_o[b]) + val : val;
                 } else {
                     const uint32_t old = (o & 1) ? pre_o[b] >> 16 : pre_o[b] & 0xFFFFu;
-                    reinterpret_cast<uint16_t *>(a.out)[o] =
+                    reinterpret_cast<uint16_t *>(cout)[o] =
                         (uint16_t)f32_to_bf16(a.accumulate ? val + bf16_to_f32(old) : val);
                 }
             }
@@ -388,13 +444,50 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         const uint32_t rows = min(a.m, 16u);
         eout = tid < 256 && erow < rows && (!kGateUp || a.partial || ecol < 8);
         orow = erow;
+        // the problem holding tile t: its fields, by value; returns its first tile
+        auto select = [&](uint32_t t) -> uint32_t {
+            const int pi = (a.nmore > 1 && t >= a.tile_begin[2]) ? 2 : (a.nmore > 0 && t >= a.tile_begin[1]) ? 1 : 0;
+            if (pi == 0) {
+                cw = a.w;
+                cout = a.out;
+                cbias = a.bias;
+                cldo = a.ldo;
+            } else {
+                const SkinnyArgs::More &mp = pi == 1 ? a.more[0] : a.more[1];
+                cw.qw = mp.w.qw;
+                cw.sc = mp.w.sc;
+                cw.bi = mp.w.bi;
+                cw.n = mp.w.n;
+                cout = mp.out;
+                cbias = mp.bias;
+                cldo = mp.ldo;
+            }
+            crows = cw.n;
+            return a.tile_begin[pi];
+        };
+        uint32_t tb = select(run_begin);
         // X loads first, then the first tile's words: the conversion waits for X only
         stage_load(0, rows);
-        fetch(B0{}, 0, run_begin);
+        fetch(B0{}, 0, run_begin - tb);
         __builtin_amdgcn_sched_barrier(0);
+        if (a.ln_w) norm_x(rows);
         stage_store(rows);
         lds_barrier();
-        run_tiles(0, run_begin, run_end);
+        // first tile of the problem after the one holding t (constant kernel-argument indices)
+        auto next_begin = [&](uint32_t t) -> uint32_t {
+            if (a.nmore > 0 && t < a.tile_begin[1]) return a.tile_begin[1];
+            if (a.nmore > 1 && t < a.tile_begin[2]) return a.tile_begin[2];
+            return a.nmore == 0 ? a.tile_begin[1] : a.nmore == 1 ? a.tile_begin[2] : a.tile_begin[3];
+        };
+        uint32_t t = run_begin;
+        for (;;) {
+            const uint32_t seg_end = min(run_end, next_begin(t));
+            run_tiles(0, t - tb, seg_end - tb);
+            t = seg_end;
+            if (t >= run_end) break;
+            tb = select(t);
+            fetch(B0{}, 0, t - tb);
+        }
         return;
     }
 
@@ -447,13 +540,22 @@ hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s) {
     const bool grouped = a.offsets != nullptr;
     a.ksplit = skinny_ksplit(a.k);
     if (grouped && a.ksplit != 1) return hipErrorInvalidValue;
+    if (grouped && (a.nmore > 0 || a.ln_w)) return hipErrorInvalidValue;
+    if (a.nmore < 0 || a.nmore > 2 || (a.nmore > 0 && (gate_up || a.partial))) return hipErrorInvalidValue;
+    if (a.ln_w && a.ksplit != 1) return hipErrorInvalidValue;  // the norm needs the whole row in the slab
+    for (int i = 0; i < a.nmore; ++i)
+        if (!skinny_supported(a.more[i].w) || a.more[i].w.k != a.k) return hipErrorInvalidValue;
+    const uint32_t tile_rows = gate_up ? 8 : 16;
     if (!grouped) {
         a.experts = 1;
         a.expert_rows = a.w.n;
         a.max_active = 1;
+        a.tile_begin[0] = 0;
+        a.tile_begin[1] = (a.w.n + tile_rows - 1) / tile_rows;
+        for (int i = 0; i < a.nmore; ++i) a.tile_begin[i + 2] = a.tile_begin[i + 1] + (a.more[i].w.n + 15) / 16;
     }
-    const uint32_t tile_rows = gate_up ? 8 : 16;
-    const uint32_t items = a.max_active * ((a.expert_rows + tile_rows - 1) / tile_rows);
+    const uint32_t items =
+        grouped ? a.max_active * ((a.expert_rows + tile_rows - 1) / tile_rows) : a.tile_begin[a.nmore + 1];
     if (gate_up) return grouped ? launch_t<true, true>(a, items, s) : launch_t<true, false>(a, items, s);
     return grouped ? launch_t<false, true>(a, items, s) : launch_t<false, false>(a, items, s);
 }

@@ -150,11 +150,12 @@ def test_rope_attention_matches_two_step_path(kq, B, H, KVH, D, ctx, pos):
     assert np.all(np.abs(g - w) <= np.abs(w) * 2.0 ** -7 + 1e-3 * np.abs(w).max())
 
 
-@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("m", [1, 3, 9, 16])
 def test_rmsnorm_fused_qkv_and_mlp(kq, m):
     """qkv(rmsnorm(h)) and h += mlp(rmsnorm(h)) against kr_rmsnorm followed by the unfused calls:
-    m = 1 fuses the norm into the GEMVs (the mean may differ in its f32 summation order, so a few
-    normalised values may round to the neighbouring bf16), m = 3 runs the norm first."""
+    m = 1 fuses the norm into the GEMVs and m = 9, 16 into the few-token kernel's staging of x (the
+    mean may differ in its f32 summation order, so a few normalised values may round to the
+    neighbouring bf16); m = 3 runs the norm first."""
     from kriya_q4 import synth
     H, I, QN, KN = 256, 512, 256, 128
     case(f"rmsnorm fused into qkv / mlp m={m}")
