@@ -141,26 +141,24 @@ def bench_gemv_cfg0(kq, torch, synth, copies, steps, warmup):
 
 
 def bench_prefill_cfg2(kq, torch, synth, copies, steps):
-    """Config 2: the seven projections of one layer at M = 512 (q/k/v fused, o, gate/up fused, down)."""
+    """Config 2: the seven projections of one layer at M = 512: q/k/v in one launch, o accumulated into the
+    residual, and the MLP entry point (gate/up + SwiGLU, then down accumulated into the residual)."""
     M, H, I, KV = 512, 2048, 11008, 256
     shapes = [(H, H), (KV, H), (KV, H), (H, H), (I, H), (I, H), (H, I)]  # q k v o gate up down
     planars = [synth.q4_weight(n, k, 2000 + i) for i, (n, k) in enumerate(shapes)]
     rot = Rotation(kq, torch, planars, copies)
     x = torch.from_numpy(synth.bf16_normal((M, H), 2100).view(np.int16)).cuda().view(torch.bfloat16)
-    xi = torch.from_numpy(synth.bf16_normal((M, I), 2101).view(np.int16)).cuda().view(torch.bfloat16)
     qo = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
     ko = torch.empty((M, KV), dtype=torch.bfloat16, device="cuda")
     vo = torch.empty((M, KV), dtype=torch.bfloat16, device="cuda")
-    oo = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
-    act = torch.empty((M, I), dtype=torch.bfloat16, device="cuda")
-    do = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    h = x.clone()  # residual stream: the o and down projections accumulate into it, as in a layer
+    ws = kq.mlp_workspace(M, H, I)
 
     def layer(i):
         q, k, v, o, g, u, d = rot.sets[i % len(rot)]
         kq.qkv(q, k, v, x, out_dtype=kq.DTYPE_BF16, outs=(qo, ko, vo))
-        kq.q4_linear(o, x, y=oo)
-        kq.gate_up_act(g, u, x, out=act)
-        kq.q4_linear(d, xi, y=do)
+        kq.q4_linear(o, x, y=h, accumulate=True)
+        kq.mlp(g, u, d, h, x=x, workspace=ws)  # gate/up + SwiGLU, then down into h (split K via the workspace)
 
     t = graph_time_per_step(torch, layer, len(rot), max(1, steps // (8 * len(rot))), 1)
     flops = sum(2 * M * n * k for n, k in shapes)

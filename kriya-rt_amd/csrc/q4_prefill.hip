@@ -359,9 +359,10 @@ static hipError_t launch_prefill_shape(MfmaArgs &a, hipStream_t s) {
 //             (96 x 128: down 145 us, o 33 us; 64 x 64: down 72 us, o 17.6 us).
 using GateUpShape = PrefillTile<8, 2, 4, 2>;
 using PlainShape = PrefillTile<4, 1, 4, 1>;
+using SplitShape = PrefillTile<6, 2, 4, 1>;  // plain projections whose K is split over blocks
 
-uint32_t prefill_block_m(bool gate_up) { return gate_up ? GateUpShape::kBM : PlainShape::kBM; }
-uint32_t prefill_block_rows(bool gate_up) { return gate_up ? GateUpShape::kBN : PlainShape::kBN; }
+uint32_t prefill_block_m(bool gate_up) { return gate_up ? GateUpShape::kBM : SplitShape::kBM; }
+uint32_t prefill_block_rows(bool gate_up) { return gate_up ? GateUpShape::kBN : SplitShape::kBN; }
 
 bool prefill_supported(const MfmaArgs &a) {
     // 32-bit buffer offsets: every operand must span < 4 GiB
@@ -376,6 +377,7 @@ bool prefill_supported(const MfmaArgs &a) {
 
 hipError_t launch_prefill(MfmaArgs &a, hipStream_t s) {
     if (a.p[0].w2.qw != nullptr) return launch_prefill_shape<8, 2, 4, 2, 3, 2>(a, s);
+    if (a.ksplit > 1) return launch_prefill_shape<6, 2, 4, 1, 4, 2>(a, s);  // split K: blocks come from the split
     return launch_prefill_shape<4, 1, 4, 1, 4, 2>(a, s);
 }
 
