@@ -82,7 +82,8 @@ const char *kr_last_error(void);
 #define KR_OPT_GEMV_BLOCK_ROWS 4        /* rows per split-K block tile: 1, 2 (default), 4, 8 */
 #define KR_OPT_GEMV_PERSISTENT_BLOCKS 5 /* grid of the persistent wave kernel (1024)       */
 #define KR_OPT_SKINNY_MAX_BLOCKS 6      /* grid cap of the few-token kernel (512)          */
-#define KR_OPT_PREFILL_KERNEL 7         /* m > 16: 0 register-dequant (default), 1 tiled */
+#define KR_OPT_PREFILL_KERNEL 7         /* m > 16: 0 register-dequant (default), 1 tiled, 2 register-dequant
+                                           with 64-column steps (0 takes 128 where k allows) */
 #define KR_OPT_GEMV_LONG_ROWS 8         /* k > 4096 rows per 1024-thread block: 4, 8 (default), 16; 0 split-K */
 #define KR_OPT_GEMV_TOKENS 9            /* 2 <= m <= 4: 1 (default) the GEMV kernels take all tokens per
                                            unpacked word (k <= 2048, or k <= 16384 without gate/up);

@@ -189,7 +189,7 @@ size_t partial_bytes(uint32_t m, uint32_t n, uint32_t k, int nw) {
 // Split K over the blocks when the tile grid alone would leave CUs idle.
 void choose_split_k(MfmaArgs &a, int bm, float *partial) {
     const uint32_t groups = a.k / 64;
-    const bool prefill = bm > 16 && tuning().prefill_kernel == 0 && prefill_supported(a);
+    const bool prefill = bm > 16 && tuning().prefill_kernel != 1 && prefill_supported(a);
     const uint32_t rows = prefill ? prefill_block_m(a.p[0].w2.qw != nullptr) : (uint32_t)bm_rows(bm);
     const uint32_t cols = prefill ? prefill_block_rows(a.p[0].w2.qw != nullptr) : (uint32_t)bn_of(bm, false);
     const uint32_t tiles = ((a.m + rows - 1) / rows) * ((a.p[0].w.n + cols - 1) / cols);
@@ -198,7 +198,7 @@ void choose_split_k(MfmaArgs &a, int bm, float *partial) {
     while (split < kMaxSplitK && tiles * split < target && groups / (split * 2) >= 8) split *= 2;
     if (split > 1) {
         a.ksplit = split;
-        a.groups_per_split = (groups + split - 1) / split;
+        a.groups_per_split = ((groups + split - 1) / split + 1) & ~1u;  // even: the prefill kernel's steps take two groups
         a.partial = partial;
     }
 }
@@ -248,7 +248,7 @@ int kr_set_option(int option, int value) {
             tuning().gemv_long_rows = value;
             return ok();
         case KR_OPT_PREFILL_KERNEL:
-            if (value != 0 && value != 1) return fail(KR_E_INVALID, "prefill kernel must be 0 or 1");
+            if (value < 0 || value > 2) return fail(KR_E_INVALID, "prefill kernel must be 0, 1 or 2");
             tuning().prefill_kernel = value;
             return ok();
         case KR_OPT_GEMV_TOKENS:

@@ -334,7 +334,7 @@ static hipError_t launch_shape(MfmaArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_mfma(MfmaArgs &a, int bm, hipStream_t s) {
-    if (bm > 16 && tuning().prefill_kernel == 0 && prefill_supported(a)) return launch_prefill(a, s);
+    if (bm > 16 && tuning().prefill_kernel != 1 && prefill_supported(a)) return launch_prefill(a, s);
     const bool gate_up = a.p[0].w2.qw != nullptr;
     if (gate_up) {
         if (bm <= 16) return launch_shape<32, 32, 2>(a, s);

@@ -117,10 +117,18 @@ struct PrefillTile {
 // vmcnt completes in issue order, so waiting for the X slice of step g + 1 at
 // the end of step g also waits for every load issued before it: with X and
 // weights requested together D steps ahead, both get D steps of latency.
-template <int MF, int NF, int WAVES, int NW, int OCC, int EPI, int D>
+// SW: quantisation groups (64 columns) per step.  With SW = 2 a lane's
+// weights of a step are one 16-byte load (32 nibbles: four MFMA slices) and
+// its scales and biases one 4-byte pair each: half the load instructions of
+// SW = 1, whose lanes load 8 bytes and two 2-byte values per 64 columns.
+template <int MF, int NF, int WAVES, int NW, int OCC, int EPI, int D, int SW>
 __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs args) {
     using T = PrefillTile<MF, NF, WAVES, NW>;
     constexpr int FPM = T::kFPM;
+    constexpr int kUnits = 8 * SW;                  // 16-byte X units per LDS row
+    constexpr int kBuf = T::kBM * 16 * kUnits;      // bytes of one X slice
+    constexpr int kSlices = 2 * SW;                 // 32-column MFMA slices per step
+    static_assert(SW == 1 || SW == 2, "one or two groups per step");
     extern __shared__ __align__(16) char lds[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -141,10 +149,11 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
     const uint32_t mt = local % tiles_m, nt = local / tiles_m;
     const uint32_t m0 = mt * T::kBM;
     const uint32_t N = P.w.n, M = args.m, K = args.k, G = K >> 6;
+    const uint32_t GS = G / SW;                                // steps over the whole row
     const uint32_t row0 = nt * T::kBN + wave * T::kWaveRows;  // first weight row of this wave
     const uint32_t ks = blockIdx.y;
-    const uint32_t g_begin = ks * args.groups_per_split;
-    const uint32_t g_end = min(G, g_begin + args.groups_per_split);
+    const uint32_t g_begin = ks * (args.groups_per_split / SW);  // in steps (groups_per_split % SW == 0)
+    const uint32_t g_end = min(GS, g_begin + args.groups_per_split / SW);
 
     const uint32_t kMask = opaque_v(0x000F000Fu);
     const uint32_t kMagic = opaque_v(0x64006400u);
@@ -164,51 +173,67 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
 #pragma unroll
     for (int f = 0; f < FPM; ++f) {
         const uint32_t row = min(row0 + f * 16 + c, N - 1);  // tail rows re-read row N-1; never stored
-        oq[f] = row * rowbytes + kq * 8;
+        oq[f] = row * rowbytes + kq * (8 * SW);
         os[f] = row * G * 2;
     }
     // ---- X staging: direct-to-LDS loads (no VGPR round trip), converted in place.
-    // A buffer holds the block's BM rows x 8 units (16 B) of one 64-column slice;
-    // row r, unit u lives in slot r * 8 + (u ^ swz(r)).  DMA instruction i of a
+    // A buffer holds the block's BM rows x kUnits units (16 B) of one step's columns;
+    // row r, unit u lives in slot r * kUnits + (u ^ swizzle(r)).  DMA instruction i of a
     // wave writes 64 consecutive slots (lane l -> slot base + l), so each lane
     // loads the global unit that belongs in its slot and later converts exactly
     // the slots it loaded (its own data: no barrier between load and convert).
-    constexpr int XI = T::kBM * 8 / 64 / WAVES;  // DMA instructions per wave per step
-    static_assert(T::kBM * 8 % (64 * WAVES) == 0, "X slice must split into whole DMA instructions");
+    auto swizzle = [](uint32_t r) -> uint32_t { return SW == 1 ? swz(r) : (r & 15); };
+    constexpr int XI = T::kBM * kUnits / 64 / WAVES;  // DMA instructions per wave per step
+    static_assert(T::kBM * kUnits % (64 * WAVES) == 0, "X slice must split into whole DMA instructions");
     const rsrc_t rx = make_rsrc(args.x, (M - 1) * args.ldx * 2 + K * 2);
     uint32_t xo[XI];
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
         const uint32_t slot = (wave * XI + i) * 64 + lane;
-        const uint32_t r = slot >> 3, u = (slot & 7) ^ swz(r);
+        const uint32_t r = slot / kUnits, u = (slot % kUnits) ^ swizzle(r);
         xo[i] = min(m0 + r, M - 1) * args.ldx * 2 + u * 16;  // tail rows re-read row M-1; never stored
     }
     auto dma_x = [&](uint32_t g, int buf) {
 #pragma unroll
-        for (int i = 0; i < XI; ++i) dma16(rx, lds + buf * T::kBufBytes + (wave * XI + i) * 1024, xo[i], g * 128);
+        for (int i = 0; i < XI; ++i) dma16(rx, lds + buf * kBuf + (wave * XI + i) * 1024, xo[i], g * (128 * SW));
     };
     auto convert_x = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < XI; ++i) {
-            u32x4 *p = reinterpret_cast<u32x4 *>(lds + buf * T::kBufBytes + (wave * XI + i) * 1024 + lane * 16);
+            u32x4 *p = reinterpret_cast<u32x4 *>(lds + buf * kBuf + (wave * XI + i) * 1024 + lane * 16);
             *p = x_unit_f16(*p);
         }
     };
-    // A fragment reads: row r = 16 * a + c (swz depends on c only), unit 2 * kq + j
-    const uint32_t xa0 = ((c * 8) + ((2 * kq + 0) ^ swz(c))) * 16;
-    const uint32_t xa1 = ((c * 8) + ((2 * kq + 1) ^ swz(c))) * 16;
+    // A fragment of slice j: row r = 16 * a + c (the swizzle depends on c only), unit
+    // 2 kq + j (SW = 1) or 4 kq + j (SW = 2): the lane's 8 columns of that slice
+    uint32_t xa[kSlices];
+#pragma unroll
+    for (int j = 0; j < kSlices; ++j)
+        xa[j] = ((c * kUnits) + (((uint32_t)kSlices * kq + j) ^ swizzle(c))) * 16;
 
     struct WRegs {
-        u32x2 q[NF];
+        uint32_t q[NF][kSlices];
         uint32_t s[NF], b[NF];
     };
     auto load_w = [&](uint32_t g, WRegs &r) {
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
             const int mi = f / FPM, fi = f % FPM;
-            r.q[f] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rq[mi], oq[fi], g * 32, 0));
-            r.s[f] = __builtin_amdgcn_raw_buffer_load_b16(rs[mi], os[fi], g * 2, 0);
-            r.b[f] = __builtin_amdgcn_raw_buffer_load_b16(rb[mi], os[fi], g * 2, 0);
+            if constexpr (SW == 1) {
+                const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rq[mi], oq[fi], g * 32, 0));
+                r.q[f][0] = v.x;
+                r.q[f][1] = v.y;
+                r.s[f] = __builtin_amdgcn_raw_buffer_load_b16(rs[mi], os[fi], g * 2, 0);
+                r.b[f] = __builtin_amdgcn_raw_buffer_load_b16(rb[mi], os[fi], g * 2, 0);
+            } else {
+                const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mi], oq[fi], g * 64, 0));
+                r.q[f][0] = v.x;
+                r.q[f][1] = v.y;
+                r.q[f][2] = v.z;
+                r.q[f][3] = v.w;
+                r.s[f] = __builtin_amdgcn_raw_buffer_load_b32(rs[mi], os[fi], g * 4, 0);  // groups 2g, 2g + 1
+                r.b[f] = __builtin_amdgcn_raw_buffer_load_b32(rb[mi], os[fi], g * 4, 0);
+            }
         }
     };
 
@@ -222,18 +247,21 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
         f16x2_t s2[NF], b2[NF];
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
-            s2[f] = f16_pair(w.s[f]);
-            b2[f] = f16_pair(w.b[f]);
+            // SW = 2: lane groups kq = 0, 1 hold columns of group 2g, kq = 2, 3 of group 2g + 1
+            const uint32_t sb = SW == 1 ? w.s[f] : (kq >= 2 ? w.s[f] >> 16 : w.s[f] & 0xFFFFu);
+            const uint32_t bb = SW == 1 ? w.b[f] : (kq >= 2 ? w.b[f] >> 16 : w.b[f] & 0xFFFFu);
+            s2[f] = f16_pair(sb);
+            b2[f] = f16_pair(bb);
         }
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < kSlices; ++j) {
             f16x8_t bf[NF];
 #pragma unroll
-            for (int f = 0; f < NF; ++f) bf[f] = dequant_pairs(j == 0 ? w.q[f].x : w.q[f].y, s2[f], b2[f], kMask, kMagic);
-            const char *ab = lds + buf * T::kBufBytes + (j == 0 ? xa0 : xa1);
+            for (int f = 0; f < NF; ++f) bf[f] = dequant_pairs(w.q[f][j], s2[f], b2[f], kMask, kMagic);
+            const char *ab = lds + buf * kBuf + xa[j];
 #pragma unroll
             for (int a = 0; a < MF; ++a) {
-                const f16x8_t af = *reinterpret_cast<const f16x8_t *>(ab + a * 2048);
+                const f16x8_t af = *reinterpret_cast<const f16x8_t *>(ab + a * 16 * kUnits * 16);
 #pragma unroll
                 for (int f = 0; f < NF; ++f)
                     acc[a][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[f], acc[a][f], 0, 0, 0);
@@ -247,9 +275,9 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
         // loads issued after the X slice of a step: its weights and the later D - 1 (X, weights) pairs
         constexpr int kAfterX = kWLoads + (D - 1) * (XI + kWLoads);
         WRegs w[NB];
-        // Requests past the last group are clamped to group G - 1 (in bounds, never used), so
+        // Requests past the last step are clamped to step GS - 1 (in bounds, never used), so
         // that every step issues the same loads and the waits are fixed counts.
-        auto gc = [&](uint32_t g) { return min(g, G - 1); };
+        auto gc = [&](uint32_t g) { return min(g, GS - 1); };
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             dma_x(gc(g_begin + d), d);
@@ -327,36 +355,40 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
     }
 }
 
-template <int MF, int NF, int WAVES, int NW, int OCC, int D>
+template <int MF, int NF, int WAVES, int NW, int OCC, int D, int SW>
 static hipError_t launch_prefill_shape(MfmaArgs &a, hipStream_t s) {
     using T = PrefillTile<MF, NF, WAVES, NW>;
-    constexpr int kLds = (D + 1) * T::kBufBytes;
+    constexpr int kLds = (D + 1) * T::kBM * 128 * SW;
     uint32_t tiles = 0;
     const uint32_t tiles_m = (a.m + T::kBM - 1) / T::kBM;
     for (int i = 0; i < a.np; ++i) {
         a.p[i].tile_begin = tiles;
         tiles += tiles_m * ((a.p[i].w.n + T::kBN - 1) / T::kBN);
     }
-    const dim3 grid(tiles, a.ksplit);
+    if (a.ksplit <= 1) a.groups_per_split = a.k / 64;
+    if (a.groups_per_split % SW != 0) return hipErrorInvalidValue;
+    const dim3 grid(tiles, a.ksplit > 1 ? a.ksplit : 1);
     if (a.ksplit > 1) {
-        hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaPartial, D>), grid, dim3(T::kThreads),
+        hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaPartial, D, SW>), grid, dim3(T::kThreads),
                            kLds, s, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         return launch_splitk_reduce(a, NW, s);
     }
-    hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaDirect, D>), grid, dim3(T::kThreads), kLds, s,
+    hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaDirect, D, SW>), grid, dim3(T::kThreads), kLds, s,
                        a);
     return hipGetLastError();
 }
 
-// Launch shapes (measured on MI355X at M = 512, K = 2048 / 11008), two steps
-// of look-ahead:
-//   gate/up: 128 token rows x (4 waves x 16 gate + 16 up rows), 3 waves per
-//            SIMD (wider or narrower tiles measured slower: 105-160 us vs 97-100 us);
-//   plain:    64 token rows x (4 waves x 16 rows), 4 waves per SIMD.  The
-//             N = 2048 projections are short of blocks with larger tiles
-//             (96 x 128: down 145 us, o 33 us; 64 x 64: down 72 us, o 17.6 us).
+// Launch shapes (measured on MI355X at M = 512, K = 2048 / 11008) with
+// 128-column steps (64-column steps where k / 64 is odd):
+//   gate/up: 128 token rows x (4 waves x 16 gate + 16 up rows), one step of
+//            look-ahead, 2 waves per SIMD (the 32 KB X slices fill the LDS);
+//   plain:    64 token rows x (4 waves x 16 rows), one step of look-ahead, 4
+//             waves per SIMD: the N = 2048 projections are short of blocks with
+//             larger tiles (96 x 128: down 145 us, o 33 us; 64 x 64: 72 / 17.6 us);
+//   split K:  96 token rows x (4 waves x 32 rows), one step of look-ahead, when
+//             the MLP's workspace lets the down projection split K over blocks.
 using GateUpShape = PrefillTile<8, 2, 4, 2>;
 using PlainShape = PrefillTile<4, 1, 4, 1>;
 using SplitShape = PrefillTile<6, 2, 4, 1>;  // plain projections whose K is split over blocks
@@ -376,9 +408,16 @@ bool prefill_supported(const MfmaArgs &a) {
 }
 
 hipError_t launch_prefill(MfmaArgs &a, hipStream_t s) {
-    if (a.p[0].w2.qw != nullptr) return launch_prefill_shape<8, 2, 4, 2, 3, 2>(a, s);
-    if (a.ksplit > 1) return launch_prefill_shape<6, 2, 4, 1, 4, 2>(a, s);  // split K: blocks come from the split
-    return launch_prefill_shape<4, 1, 4, 1, 4, 2>(a, s);
+    const bool gate_up = a.p[0].w2.qw != nullptr;
+    const uint32_t gps = a.ksplit > 1 ? a.groups_per_split : a.k / 64;
+    if (tuning().prefill_kernel == 2 || a.k % 128 != 0 || gps % 2 != 0) {  // 64 columns per step
+        if (gate_up) return launch_prefill_shape<8, 2, 4, 2, 3, 2, 1>(a, s);
+        if (a.ksplit > 1) return launch_prefill_shape<6, 2, 4, 1, 4, 2, 1>(a, s);
+        return launch_prefill_shape<4, 1, 4, 1, 4, 2, 1>(a, s);
+    }
+    if (gate_up) return launch_prefill_shape<8, 2, 4, 2, 2, 1, 2>(a, s);
+    if (a.ksplit > 1) return launch_prefill_shape<6, 2, 4, 1, 2, 1, 2>(a, s);
+    return launch_prefill_shape<4, 1, 4, 1, 4, 1, 2>(a, s);
 }
 
 }  // namespace kr

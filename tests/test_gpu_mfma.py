@@ -119,9 +119,10 @@ def test_mlp_batched_split_k_is_deterministic(kq):
     assert_rms_close(runs[0] - O.bf16_to_f32(h0), delta, what="mlp B=16")
 
 
-@pytest.mark.parametrize("m,n,k", [(17, 200, 256), (40, 72, 640), (130, 300, 128)])
+@pytest.mark.parametrize("m,n,k", [(17, 200, 256), (40, 72, 640), (130, 300, 128), (33, 48, 192), (70, 130, 320)])
 def test_gate_up_prefill_tails(kq, m, n, k):
-    """m > 16 runs the prefill kernel: token-row and weight-row tails that end inside a tile."""
+    """m > 16 runs the prefill kernel: token-row and weight-row tails that end inside a tile; k = 192
+    and 320 (odd group counts) take the 64-column steps, the others 128-column steps."""
     s = synth()
     case(f"prefill gate_up tails m={m} n={n} k={k}")
     g, u = s.q4_weight(n, k, 2500 + n), s.q4_weight(n, k, 2501 + n)
@@ -161,10 +162,13 @@ def test_prefill_kernels_agree(kq, m):
     x = dev_bf16(s.bf16_normal((m, 2048), 2701))
     w = q4_dev(kq, wq)
     lib = kq.lib()
+    outs = {}
     try:
-        lib.kr_set_option(kq.OPT_PREFILL_KERNEL, 1)
-        ref = kq.q4_linear(w, x, out_dtype=kq.DTYPE_F32).cpu().numpy()
+        for opt in (1, 2):  # the tiled kernel; the prefill kernel with 64-column steps
+            assert lib.kr_set_option(kq.OPT_PREFILL_KERNEL, opt) == 0
+            outs[opt] = kq.q4_linear(w, x, out_dtype=kq.DTYPE_F32).cpu().numpy()
     finally:
         lib.kr_set_option(kq.OPT_PREFILL_KERNEL, 0)
     got = kq.q4_linear(w, x, out_dtype=kq.DTYPE_F32).cpu().numpy()
-    assert np.max(np.abs(got - ref)) <= 1e-4 * rms(ref)
+    for opt, ref in outs.items():
+        assert np.max(np.abs(got - ref)) <= 1e-4 * rms(ref), f"option {opt}"
