@@ -125,6 +125,24 @@ def bench_mlp(kq, torch, synth, B, copies, steps, warmup):
     return out
 
 
+def stream_floor(kq, torch, nbytes, copies, steps, warmup):
+    """Seconds per plain read of nbytes (kr_stream_read: 16-byte non-temporal loads, nothing else) over
+    `copies` rotating buffers, timed like the kernels: the floor for a read of that size on this GPU."""
+    n = (nbytes + 15) // 16 * 16
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    bufs = [torch.randint(-(2 ** 31), 2 ** 31 - 1, (n // 4,), dtype=torch.int32, device="cuda", generator=gen)
+            for _ in range(copies)]
+    sink = torch.empty(int(kq.lib().kr_stream_read_sink_words(n)), dtype=torch.int32, device="cuda")
+
+    def rd(i):
+        kq.stream_read(bufs[i % copies], sink)
+
+    t = graph_time_per_step(torch, rd, copies, max(1, steps // copies), max(1, warmup // copies))
+    del bufs
+    return t
+
+
 def bench_gemv_cfg0(kq, torch, synth, copies, steps, warmup):
     N, K = 11008, 2048
     rot = Rotation(kq, torch, [synth.q4_weight(N, K, 0)], copies)
@@ -321,10 +339,16 @@ def main():
                      "alg_bytes_per_launch": dom["alg_bytes"], "avg_launch_us": round(dom["s"] * 1e6, 3)},
         "cpu_baseline": None,
     }
+    log("streaming floor (plain reads of the same byte counts)")
+    floors = {k: stream_floor(kq, torch, v["alg_bytes"], args.copies, args.steps, args.warmup)
+              for k, v in head["kernels"].items()}
+    result["roofline"]["stream_floor_us"] = round(floors["gate_up_act"] * 1e6, 3)
+    result["roofline"]["frac_of_stream_floor"] = round(floors["gate_up_act"] / dom["s"], 4)
     extra = {"cfg1_B1": {"step_us": round(head["s_per_step"] * 1e6, 3), "gbs": round(head["gbs"], 1),
                          "frac_hbm": round(head["gbs"] / HBM_PEAK_GBS, 4),
                          "kernels_us": {k: round(v["s"] * 1e6, 3) for k, v in head["kernels"].items()},
-                         "kernels_gbs": {k: round(v["gbs"], 1) for k, v in head["kernels"].items()}}}
+                         "kernels_gbs": {k: round(v["gbs"], 1) for k, v in head["kernels"].items()},
+                         "stream_floor_us": {k: round(v * 1e6, 3) for k, v in floors.items()}}}
     if not args.quick:
         log("cfg0 GEMV")
         g0 = bench_gemv_cfg0(kq, torch, synth, args.copies * 3, args.steps, args.warmup)

@@ -84,12 +84,14 @@ const char *kr_last_error(void);
 #define KR_OPT_SKINNY_MAX_BLOCKS 6      /* grid cap of the few-token kernel (512)          */
 #define KR_OPT_PREFILL_KERNEL 7         /* m > 16: 0 register-dequant (default), 1 tiled, 2 register-dequant
                                            with 64-column steps (0 takes 128 where k allows) */
-#define KR_OPT_GEMV_LONG_ROWS 8         /* k > 4096 rows per 1024-thread block: 4, 8 (default), 16; 0 split-K */
+#define KR_OPT_GEMV_LONG_ROWS 8         /* k > 4096 rows per long-row block: 4, 8 (default), 16; 0 split-K */
 #define KR_OPT_GEMV_TOKENS 9            /* 2 <= m <= 4: 1 (default) the GEMV kernels take all tokens per
                                            unpacked word (k <= 2048, or k <= 16384 without gate/up);
                                            0 the few-token MFMA kernel */
 #define KR_OPT_MOE_GEMV 10              /* kr_q4_moe_experts with tokens * topk <= 16: 1 (default) one GEMV
                                            per (expert, token) pair, 0 the grouped MFMA kernel */
+#define KR_OPT_GEMV_LONG_GROUPS 11      /* long-row kernel: row groups of 512 threads per block, each
+                                           taking rows / groups of the block's rows: 1 or 2 (default) */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 
@@ -222,6 +224,14 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
  * out: bf16 [count, w->k], 2-byte aligned. */
 int kr_q4_embedding(const kr_q4_matrix *w, const uint32_t *tokens, uint32_t count, uint16_t *out,
                     void *stream);
+
+/* ---- measurement helper (no counterpart in the reference) ----
+ * A plain read of `bytes` bytes of device memory, the floor the GEMV kernels are
+ * compared with at the same byte count.  sink[i] = xor of the 32-bit words of
+ * the i-th 16 KB of buf; sink holds kr_stream_read_sink_words(bytes) words.
+ * buf 16-byte aligned, bytes a multiple of 16 (> 0). */
+size_t kr_stream_read_sink_words(size_t bytes);
+int kr_stream_read(const void *buf, size_t bytes, uint32_t *sink, void *stream);
 
 #ifdef __cplusplus
 }

@@ -297,45 +297,58 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
     const uint32_t s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, splits = gridDim.x;
     const uint32_t G = q_heads / kv_heads, half = D / 2, P = D / 8;
     const uint32_t p0 = s * kSplitLen;
+    // The position first: loads complete in issue order, so it can arrive (and the RoPE table row
+    // it selects be requested) while the key and value rows below are still in flight.
+    const uint32_t pos = __builtin_amdgcn_readfirstlane(positions[b]);
+    __builtin_amdgcn_sched_barrier(0);
     // 0. loads that do not depend on the position, all in one round trip with it: the key piece
     //    (position p0 + r, piece c [+16]) and value piece (position p0 + c, piece r [+16]) of rows
     //    below max_ctx, two query pairs per thread, and the new k and v pairs of thread < D/2.
     const size_t row_stride = (size_t)kv_heads * D;
     const uint16_t *kbase = k_cache + (((size_t)b * max_ctx + p0) * kv_heads + kvh) * D;
     const uint16_t *vbase = v_cache + (((size_t)b * max_ctx + p0) * kv_heads + kvh) * D;
+    // Loads are unconditional, from clamped (in-bounds) addresses; what they should not
+    // contribute is zeroed where it is used.  A conditional load merged with a default value
+    // makes the compiler wait for every load in flight at the merge.
+    const uint32_t kr_ = p0 + r < max_ctx ? r : 0u, vc_ = p0 + c < max_ctx ? c : 0u;
     u32x4 kw[2], vw[2];
-#pragma unroll
-    for (uint32_t j = 0; j < 2; ++j) {
-        kw[j] = u32x4{0, 0, 0, 0};
-        vw[j] = u32x4{0, 0, 0, 0};
-        if (p0 + r < max_ctx && c + 16 * j < P)
-            kw[j] = *reinterpret_cast<const u32x4 *>(kbase + r * row_stride + 8 * (c + 16 * j));
-        if (p0 + c < max_ctx && r + 16 * j < P)
-            vw[j] = *reinterpret_cast<const u32x4 *>(vbase + c * row_stride + 8 * (r + 16 * j));
+    kw[0] = *reinterpret_cast<const u32x4 *>(kbase + kr_ * row_stride + 8 * min(c, P - 1));
+    vw[0] = *reinterpret_cast<const u32x4 *>(vbase + vc_ * row_stride + 8 * min(r, P - 1));
+    kw[1] = vw[1] = u32x4{0, 0, 0, 0};
+    if (P > 16) {  // rows of D > 128: a second piece (uniform)
+        kw[1] = *reinterpret_cast<const u32x4 *>(kbase + kr_ * row_stride + 8 * min(c + 16, P - 1));
+        vw[1] = *reinterpret_cast<const u32x4 *>(vbase + vc_ * row_stride + 8 * min(r + 16, P - 1));
     }
     constexpr uint32_t kQPairs = GP * kGlueMaxHeadDim / 2 / 256;  // query pairs per thread: G * D/2 <= 256 max(kQPairs, 1)
     uint32_t qraw[kQPairs > 0 ? kQPairs : 1][2];
 #pragma unroll
     for (uint32_t j = 0; j < (kQPairs > 0 ? kQPairs : 1); ++j) {
-        const uint32_t i = tid + 256 * j, g = i / half, d = i % half;
-        qraw[j][0] = qraw[j][1] = 0;
-        if (i < G * half) {
-            const uint16_t *src = q + ((size_t)b * q_heads + kvh * G + g) * D;
-            qraw[j][0] = src[d];
-            qraw[j][1] = src[d + half];
-        }
+        const uint32_t i0 = tid + 256 * j, i = i0 < G * half ? i0 : 0u, g = i / half, d = i % half;
+        const uint16_t *src = q + ((size_t)b * q_heads + kvh * G + g) * D;
+        qraw[j][0] = src[d];
+        qraw[j][1] = src[d + half];
     }
-    uint32_t kn0 = 0, kn1 = 0, vn0 = 0, vn1 = 0;
-    if (tid < half) {
+    uint32_t kn0, kn1, vn0, vn1;
+    {
+        const uint32_t tn = tid < half ? tid : 0u;
         const uint16_t *ks = k + ((size_t)b * kv_heads + kvh) * D;
         const uint16_t *vs = v + ((size_t)b * kv_heads + kvh) * D;
-        kn0 = ks[tid];
-        kn1 = ks[tid + half];
-        vn0 = vs[tid];
-        vn1 = vs[tid + half];
+        kn0 = ks[tn];
+        kn1 = ks[tn + half];
+        vn0 = vs[tn];
+        vn1 = vs[tn + half];
     }
-    const uint32_t pos = positions[b];
     const bool append = pos < max_ctx;
+    // the RoPE table row of the new position: requested as soon as the position is here (a
+    // scalar load), not after the key and value rows issued above have arrived
+    const float2 *trow = reinterpret_cast<const float2 *>(cos_sin) + (size_t)(append ? pos : 0u) * half;
+    float2 tq[kQPairs > 0 ? kQPairs : 1];
+#pragma unroll
+    for (uint32_t j = 0; j < (kQPairs > 0 ? kQPairs : 1); ++j) {
+        const uint32_t i0 = tid + 256 * j, i = i0 < G * half ? i0 : 0u;
+        tq[j] = trow[i % half];
+    }
+    const float2 tk = trow[tid < half ? tid : 0u];
     const uint32_t n = min(pos, max_ctx - 1) + 1;
     const uint32_t p1 = min(n, p0 + kSplitLen);
     float *out = part + (((size_t)b * kv_heads + kvh) * splits + s) * (size_t)G * (D + 2);  // m[G], l[G], acc[G][D]
@@ -354,7 +367,7 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
         if (i < G * half) {
             float x0 = bf16_to_f32(qraw[j][0]), x1 = bf16_to_f32(qraw[j][1]);
             if (append) {
-                const float2 t = reinterpret_cast<const float2 *>(cos_sin)[(size_t)pos * half + d];
+                const float2 t = tq[j];
                 const float r0 = fmaf(x0, t.x, -x1 * t.y), r1 = fmaf(x0, t.y, x1 * t.x);
                 x0 = bf16_round(r0);
                 x1 = bf16_round(r1);
@@ -369,7 +382,7 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
         if (p0 + c >= p1) vw[j] = u32x4{0, 0, 0, 0};
     // 2. the new key (rotated) and value, into LDS for this block's own use (the cache is written at the end)
     if (has_new && tid < half) {
-        const float2 t = reinterpret_cast<const float2 *>(cos_sin)[(size_t)pos * half + tid];
+        const float2 t = tk;
         const float x0 = bf16_to_f32(kn0), x1 = bf16_to_f32(kn1);
         const uint32_t k0 = f32_to_bf16(fmaf(x0, t.x, -x1 * t.y)), k1 = f32_to_bf16(fmaf(x0, t.y, x1 * t.x));
         knew[tid] = bf16_to_f32(k0);
@@ -529,14 +542,20 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float *par
     float M = -INFINITY, L = 0.0f, acc = 0.0f;
     for (uint32_t s0 = 0; s0 < splits; s0 += round) {
         const uint32_t cnt = min(round, splits - s0);
+        const float *rb = base + (size_t)s0 * stride;
+        // (m, l) first and unconditional (clamped row; what it should not contribute is dropped
+        // below): a conditional load merged with a default value after the value loads would make
+        // the compiler wait for all of them before issuing it -- a second round trip.
+        const float mraw = rb[min(tid, cnt - 1) * stride + g];
+        const float lraw = rb[min(tid, cnt - 1) * stride + G + g];
         float a[kPer];
 #pragma unroll
         for (uint32_t j = 0; j < kPer; ++j) {
             const uint32_t sj = il + j * NI;
-            a[j] = (il < NI && sj < cnt) ? base[(s0 + sj) * stride + 2 * G + g * D + d] : 0.0f;
+            a[j] = (il < NI && sj < cnt) ? rb[sj * stride + 2 * G + g * D + d] : 0.0f;
         }
-        const float mt = tid < cnt ? base[(s0 + tid) * stride + g] : -INFINITY;
-        const float lt = tid < cnt ? base[(s0 + tid) * stride + G + g] : 0.0f;
+        const float mt = tid < cnt ? mraw : -INFINITY;
+        const float lt = tid < cnt ? lraw : 0.0f;
         const float Mc = fmaxf(M, block_max256(mt, r4));
         const float wt = mt == -INFINITY ? 0.0f : expf(mt - Mc);
         sw[tid] = wt;

@@ -259,6 +259,10 @@ int kr_set_option(int option, int value) {
             if (value != 0 && value != 1) return fail(KR_E_INVALID, "moe gemv must be 0 or 1");
             tuning().moe_gemv = value;
             return ok();
+        case KR_OPT_GEMV_LONG_GROUPS:
+            if (value != 1 && value != 2) return fail(KR_E_INVALID, "long-row groups must be 1 or 2");
+            tuning().gemv_long_groups = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -275,8 +279,19 @@ int kr_get_option(int option) {
         case KR_OPT_GEMV_LONG_ROWS: return tuning().gemv_long_rows;
         case KR_OPT_GEMV_TOKENS: return tuning().gemv_tokens;
         case KR_OPT_MOE_GEMV: return tuning().moe_gemv;
+        case KR_OPT_GEMV_LONG_GROUPS: return tuning().gemv_long_groups;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
+}
+
+size_t kr_stream_read_sink_words(size_t bytes) { return stream_read_sink_words(bytes); }
+
+int kr_stream_read(const void *buf, size_t bytes, uint32_t *sink, void *stream) {
+    if (!buf || !sink) return fail(KR_E_INVALID, "buf and sink must not be NULL");
+    if (bytes == 0 || bytes % 16 != 0) return fail(KR_E_SHAPE, "bytes must be a positive multiple of 16");
+    if (!aligned(buf, 16) || !aligned(sink, 4)) return fail(KR_E_ALIGN, "buf must be 16-byte aligned, sink 4-byte");
+    if (stream_read_sink_words(bytes) > 0x7FFFFFFFu) return fail(KR_E_SHAPE, "bytes too large");
+    return hip_status(launch_stream_read(buf, bytes, sink, (hipStream_t)stream), "kr_stream_read");
 }
 
 int kr_q4_dequant(const kr_q4_matrix *w, float *out, void *stream) {

@@ -32,8 +32,9 @@ struct Tuning {
     int skinny_max_blocks = 512;       // grid cap of the few-token kernel (blocks walk runs of tiles)
     int prefill_kernel = 0;            // m > 16: 0 = register-dequant prefill kernel,
                                        // 1 = LDS-dequant tiled kernel
-    int gemv_long_rows = 8;            // k > 4096: rows per 1024-thread block of the long-row kernels (4, 8, 16);
+    int gemv_long_rows = 8;            // k > 4096: rows per block of the long-row kernels (4, 8, 16);
                                        // 0 = split-K block kernel
+    int gemv_long_groups = 2;          // long-row kernel: row groups of 512 threads per block (1, 2)
     int gemv_tokens = 1;               // 2 <= m <= 4: GEMV kernels over the tokens (1) or the few-token
                                        // MFMA kernel (0)
     int moe_gemv = 1;                  // MoE with <= 16 assignments: routed GEMV (1) or grouped MFMA kernel (0)
@@ -44,6 +45,8 @@ Tuning &tuning();
 constexpr uint32_t kMaxGemvK = 3 * 256 * 32;
 
 hipError_t launch_format_dequant(const Q4Mat &w, float *out, hipStream_t s);
+size_t stream_read_sink_words(size_t bytes);
+hipError_t launch_stream_read(const void *buf, size_t bytes, uint32_t *sink, hipStream_t s);
 hipError_t launch_from_blocks36(const void *blocks, uint32_t n, uint32_t k, uint32_t *qw, uint16_t *sc,
                                 uint16_t *bi, hipStream_t s);
 hipError_t launch_to_blocks36(const Q4Mat &w, void *blocks, hipStream_t s);

@@ -146,17 +146,17 @@ __global__ __launch_bounds__(256) void q4_gemv_block_kernel(Q4Mat A, Q4Mat B, co
 // (butterfly, then the 8 waves of the group in order).
 // M > 1: x holds M token rows; thread (g, c) multiplies its words with the
 // chunk c of every token and the block stores M rows of outputs.
-template <int RB, int EPI, int M = 1>
-__global__ __launch_bounds__(1024) void q4_gemv_rows_kernel(Q4Mat A, const uint16_t *__restrict__ x, GemvOut o) {
-    constexpr int RPG = RB / 2;
+template <int RB, int EPI, int M = 1, int NG = 2>
+__global__ __launch_bounds__(NG * 512) void q4_gemv_rows_kernel(Q4Mat A, const uint16_t *__restrict__ x, GemvOut o) {
+    constexpr int RPG = RB / NG;
     constexpr int MP = tokens_pow2<M>();
     constexpr int kVals = RPG * MP;  // values per thread: (row i of the group, token), tokens padded
     constexpr int kSeg = kWave / kVals;
-    __shared__ float red[2][8][kVals];
+    __shared__ float red[NG][8][kVals];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const uint32_t g = wave >> 3, c = (wave & 7) * kWave + lane;
+    const uint32_t g = NG == 1 ? 0u : wave >> 3, c = (wave & 7) * kWave + lane;
     const uint32_t r0 = blockIdx.x * RB;
     const uint32_t nchunks = A.k >> 5, wpr = A.k >> 3, groups = A.k >> 6;
     const uint32_t kMask = sgpr_const(0x000F000Fu);
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(1024) void q4_gemv_rows_kernel(Q4Mat A, const uint1
         uint32_t sv[RPG], bv[RPG];
 #pragma unroll
         for (int i = 0; i < RPG; ++i) {
-            uint32_t row = r0 + g + 2 * i;
+            uint32_t row = r0 + g + NG * i;
             row = row < A.n ? row : A.n - 1;  // tail rows re-read a valid row and are never stored
             wv[i] = ld_stream(reinterpret_cast<const u32x4 *>(A.qw + (size_t)row * wpr) + c);
             sv[i] = ld_stream(A.sc + (size_t)row * groups + (c >> 1));
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(1024) void q4_gemv_rows_kernel(Q4Mat A, const uint1
     __syncthreads();
     if (tid < RB * M && out_row < A.n) {
         const uint32_t rr = (uint32_t)tid % RB;
-        const uint32_t gg = rr & 1, v = (rr >> 1) * MP + out_tok;
+        const uint32_t gg = rr % NG, v = (rr / NG) * MP + out_tok;
         float sum = 0.0f;
 #pragma unroll
         for (int w = 0; w < 8; ++w) sum += red[gg][w][v];
@@ -278,12 +278,18 @@ static hipError_t launch_epi(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, 
     if constexpr (!kGateUp) {
         if (lr > 0 && chunks > 128 && chunks <= 512 && tuning().gemv_split_k_chunks == 0) {
             const uint32_t blocks = (a.n + lr - 1) / lr;
-            if (lr == 4)
-                hipLaunchKernelGGL((q4_gemv_rows_kernel<4, EPI>), dim3(blocks), dim3(1024), 0, s, a, x, o);
-            else if (lr == 16)
-                hipLaunchKernelGGL((q4_gemv_rows_kernel<16, EPI>), dim3(blocks), dim3(1024), 0, s, a, x, o);
-            else
-                hipLaunchKernelGGL((q4_gemv_rows_kernel<8, EPI>), dim3(blocks), dim3(1024), 0, s, a, x, o);
+#define KR_ROWS(RB, NG) \
+    hipLaunchKernelGGL((q4_gemv_rows_kernel<RB, EPI, 1, NG>), dim3(blocks), dim3(NG * 512), 0, s, a, x, o)
+            if (tuning().gemv_long_groups == 1) {
+                if (lr == 4) KR_ROWS(4, 1);
+                else if (lr == 16) KR_ROWS(16, 1);
+                else KR_ROWS(8, 1);
+            } else {
+                if (lr == 4) KR_ROWS(4, 2);
+                else if (lr == 16) KR_ROWS(16, 2);
+                else KR_ROWS(8, 2);
+            }
+#undef KR_ROWS
             return hipGetLastError();
         }
     }

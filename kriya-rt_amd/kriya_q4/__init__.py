@@ -32,6 +32,7 @@ OPT_GEMV_BLOCK_ROWS, OPT_GEMV_PERSISTENT_BLOCKS, OPT_SKINNY_MAX_BLOCKS, OPT_PREF
 OPT_GEMV_LONG_ROWS = 8
 OPT_GEMV_TOKENS = 9
 OPT_MOE_GEMV = 10
+OPT_GEMV_LONG_GROUPS = 11
 
 _lib = None
 
@@ -66,6 +67,8 @@ def lib():
             "kr_set_option": (i32, [i32, i32]),
             "kr_get_option": (i32, [i32]),
             "kr_q4_dequant": (i32, [M, vp, vp]),
+            "kr_stream_read_sink_words": (sz, [sz]),
+            "kr_stream_read": (i32, [vp, sz, vp, vp]),
             "kr_q4_from_blocks36": (i32, [vp, u32, u32, vp, vp, vp, vp]),
             "kr_q4_to_blocks36": (i32, [M, vp, vp]),
             "kr_f16_to_bf16": (i32, [vp, vp, sz, vp]),
@@ -401,6 +404,17 @@ def argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None
         out = torch.empty(rows, dtype=torch.int32, device=logits.device)
     _check(lib().kr_argmax(_ptr(logits), rows, n, _ptr(out), _stream(stream)))
     return out
+
+
+def stream_read(buf: torch.Tensor, sink: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Measurement helper (no reference counterpart): a plain read of buf's bytes.
+    sink[i] (int32) = xor of the 32-bit words of the i-th 16 KB of buf."""
+    nbytes = buf.numel() * buf.element_size()
+    words = int(lib().kr_stream_read_sink_words(nbytes))
+    if sink is None:
+        sink = torch.empty(words, dtype=torch.int32, device=buf.device)
+    _check(lib().kr_stream_read(_ptr(buf), nbytes, _ptr(sink), _stream(stream)))
+    return sink
 
 
 # ---- names of the reference operator surface (encoder.rs) -------------------------------

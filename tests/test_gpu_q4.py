@@ -135,6 +135,46 @@ def test_gemv_shapes(kq, n, k):
         assert_rms_close(y, want, what=f"n={n} k={k} rows/wave={rpw}")
 
 
+@pytest.mark.parametrize("n,k", [(37, 4160), (2048, 11008), (100, 16384)])
+def test_gemv_long_row_kernel_options(kq, n, k):
+    """The long-row kernel (4096 < k <= 16384) at every rows-per-block / row-group setting: each matches the
+    oracle, and all give the same bits (one chunk per lane and a fixed reduction order in every setting)."""
+    s = synth()
+    case(f"gemv long rows n={n} k={k}, rows per block 4/8/16 x row groups 1/2")
+    wq = s.q4_weight(n, k, 500 + n)
+    x = s.bf16_normal((1, k), 501 + n)
+    want = O.q4_matmul(O.Q4Planar(*wq), x)[0]
+    w, xd = q4_dev(kq, wq), dev_bf16(x)
+    outs = {}
+    try:
+        for groups in (1, 2):
+            for rows in (4, 8, 16):
+                kq.set_option(kq.OPT_GEMV_LONG_ROWS, rows)
+                kq.set_option(kq.OPT_GEMV_LONG_GROUPS, groups)
+                outs[(groups, rows)] = kq.q4_linear(w, xd, out_dtype=kq.DTYPE_F32).cpu().numpy()[0]
+    finally:
+        kq.set_option(kq.OPT_GEMV_LONG_ROWS, 8)
+        kq.set_option(kq.OPT_GEMV_LONG_GROUPS, 2)
+    for key, y in outs.items():
+        assert_rms_close(y, want, what=f"groups={key[0]} rows={key[1]}")
+        assert np.array_equal(y.view(np.uint32), outs[(2, 8)].view(np.uint32)), key
+
+
+def test_stream_read_xor_per_block(kq):
+    """The streaming-floor helper reads every byte: sink[i] = xor of the words of the i-th 16 KB."""
+    case("stream_read 3 x 16 KB + 48 B")
+    rng = np.random.default_rng(5)
+    words = rng.integers(0, 2 ** 32, size=(3 * 16384 + 48) // 4, dtype=np.uint32)
+    buf = torch.from_numpy(words.view(np.int32)).cuda()
+    sink = kq.stream_read(buf).cpu().numpy().view(np.uint32)
+    per = 16384 // 4
+    want = [np.bitwise_xor.reduce(words[i:i + per]) for i in range(0, words.size, per)]
+    assert sink.size == len(want) == 4
+    assert np.array_equal(sink, np.array(want, dtype=np.uint32))
+    with pytest.raises(kq.KrError):
+        kq.stream_read(buf[:3])  # 12 bytes: not a multiple of 16
+
+
 def test_gemv_accumulate_modes(kq):
     s = synth()
     case("gemv accumulate f32 and bf16 (cfg1 down shape 2048x11008)")
