@@ -60,7 +60,8 @@ int kr_rmsnorm_q4_qkv(const uint16_t *h, const uint16_t *ln_weight, float eps, c
 
 /* h += mlp(rmsnorm(h)) for bf16 h [m, hidden] updated in place (kr_q4_mlp with
  * x = rmsnorm(h)).  m == 1 with hidden <= 4096: the norm is fused into the
- * gate/up GEMV.  workspace: kr_rmsnorm_q4_mlp_workspace_bytes(m, hidden, inter). */
+ * gate/up GEMV.  workspace: kr_rmsnorm_q4_mlp_workspace_bytes(m, hidden, inter),
+ * zero-filled once before its first use, as kr_q4_mlp's. */
 size_t kr_rmsnorm_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermediate);
 int kr_rmsnorm_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, uint16_t *h,
                       const uint16_t *ln_weight, float eps, uint32_t m, int activation, void *workspace,

@@ -92,6 +92,9 @@ const char *kr_last_error(void);
                                            per (expert, token) pair, 0 the grouped MFMA kernel */
 #define KR_OPT_GEMV_LONG_GROUPS 11      /* long-row kernel: row groups of 512 threads per block, each
                                            taking rows / groups of the block's rows: 1 or 2 (default) */
+#define KR_OPT_SPLITK_TICKETS 12        /* kr_q4_mlp at 2 <= m <= 16: 1 (default) the down projection's
+                                           K split is reduced by the last block of each run (one launch),
+                                           0 by a second launch */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 
@@ -160,7 +163,9 @@ int kr_q4_qkv(const kr_q4_matrix *q, const kr_q4_matrix *k, const kr_q4_matrix *
  * workspace: device memory of at least
  * kr_q4_mlp_workspace_bytes(m, gate->k, gate->n), 16-byte aligned; calls that
  * share a workspace must not overlap in time.  For m > 1 the workspace also
- * holds split-K partial sums of the down projection, reduced in a fixed order. */
+ * holds split-K partial sums of the down projection, reduced in a fixed order,
+ * and the counters that pick the block that reduces them: zero-fill the
+ * workspace once before its first use (every call leaves them zero). */
 size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermediate);
 int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down,
               const uint16_t *x, void *h, int h_dtype, uint32_t m, int activation,

@@ -112,10 +112,12 @@ MfmaProblem problem(const Q4Mat &w, const Q4Mat *w2, void *out, const uint16_t *
 
 // Few-token matmul on the skinny kernel.  `partial` (f32 [ksplit, m, nw * n])
 // is needed when the K split exceeds one block; without it the caller must use
-// another path (returns hipErrorInvalidValue).
+// another path (returns hipErrorInvalidValue).  `tickets` (kSkinnyTickets zero
+// words, left zero): the split is reduced inside the launch, else by a second one.
 hipError_t run_skinny(const Q4Mat &w, const Q4Mat *w2, const uint16_t *x, uint32_t m, void *out,
                       const uint16_t *bias, uint32_t ldo, int out_dtype, int accumulate, int act, float *partial,
-                      hipStream_t s, const uint16_t *ln_w = nullptr, float eps = 0.0f) {
+                      hipStream_t s, const uint16_t *ln_w = nullptr, float eps = 0.0f,
+                      uint32_t *tickets = nullptr) {
     SkinnyArgs a{};
     a.ln_w = ln_w;
     a.eps = eps;
@@ -135,9 +137,10 @@ hipError_t run_skinny(const Q4Mat &w, const Q4Mat *w2, const uint16_t *x, uint32
     if (ks > 1) {
         if (!partial) return hipErrorInvalidValue;
         a.partial = partial;
+        if (tickets && tuning().splitk_tickets && ks <= kSkinnyMaxTicketSplit) a.tickets = tickets;
     }
     hipError_t e = launch_skinny(a, s);
-    if (e != hipSuccess || ks == 1) return e;
+    if (e != hipSuccess || ks == 1 || a.tickets) return e;
     MfmaArgs r{};
     r.p[0].w = w;
     r.p[0].out = out;
@@ -263,6 +266,10 @@ int kr_set_option(int option, int value) {
             if (value != 1 && value != 2) return fail(KR_E_INVALID, "long-row groups must be 1 or 2");
             tuning().gemv_long_groups = value;
             return ok();
+        case KR_OPT_SPLITK_TICKETS:
+            if (value != 0 && value != 1) return fail(KR_E_INVALID, "split-K tickets must be 0 or 1");
+            tuning().splitk_tickets = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -280,6 +287,7 @@ int kr_get_option(int option) {
         case KR_OPT_GEMV_TOKENS: return tuning().gemv_tokens;
         case KR_OPT_MOE_GEMV: return tuning().moe_gemv;
         case KR_OPT_GEMV_LONG_GROUPS: return tuning().gemv_long_groups;
+        case KR_OPT_SPLITK_TICKETS: return tuning().splitk_tickets;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -431,7 +439,10 @@ int kr_q4_qkv(const kr_q4_matrix *q, const kr_q4_matrix *k, const kr_q4_matrix *
 
 size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermediate) {
     size_t bytes = round_up((size_t)m * intermediate * 2, 256);
-    if (m > 1) bytes += partial_bytes(m, hidden, intermediate, 1);  // split-K partials of the down projection
+    if (m > 1) {
+        bytes += partial_bytes(m, hidden, intermediate, 1);  // split-K partials of the down projection
+        bytes += round_up((size_t)kSkinnyTickets * 4, 256);   // and its tickets (zero between calls)
+    }
     return bytes;
 }
 
@@ -442,11 +453,13 @@ static int mlp_down(const kr_q4_matrix *gate, const kr_q4_matrix *down, const ui
     if (m == 1 || (tuning().gemv_tokens && gemv_tokens_supported(m, gate->k, true) &&
                    gemv_tokens_supported(m, down->k, false)))
         return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
-    // down projection: few N tiles at small m, so K is split over blocks; partials live in the workspace
+    // down projection: few N tiles at small m, so K is split over blocks; partials (and the
+    // tickets of the in-launch reduction) live in the workspace
     float *partial = (float *)((char *)workspace + round_up((size_t)m * gate->n * 2, 256));
+    uint32_t *tickets = (uint32_t *)((char *)partial + partial_bytes(m, gate->k, gate->n, 1));
     if (skinny_fits(m, to_mat(down), true))
         return hip_status(run_skinny(to_mat(down), nullptr, act, m, h, nullptr, down->n, h_dtype, 1, 0, partial,
-                                     (hipStream_t)stream),
+                                     (hipStream_t)stream, nullptr, 0.0f, tickets),
                           "kr_q4_mlp (down)");
     MfmaArgs args = mfma_args(act, m, down->k, h_dtype, 1);
     args.p[0] = problem(to_mat(down), nullptr, h, nullptr, down->n);

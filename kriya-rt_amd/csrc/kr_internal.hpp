@@ -38,6 +38,7 @@ struct Tuning {
     int gemv_tokens = 1;               // 2 <= m <= 4: GEMV kernels over the tokens (1) or the few-token
                                        // MFMA kernel (0)
     int moe_gemv = 1;                  // MoE with <= 16 assignments: routed GEMV (1) or grouped MFMA kernel (0)
+    int splitk_tickets = 1;            // few-token split K: 1 the last block of a run reduces, 0 a second launch
 };
 Tuning &tuning();
 
@@ -100,6 +101,8 @@ struct SkinnyArgs {
     uint32_t ldo;
     int act, out_f32, accumulate;
     float *partial;         // [ksplit, m, nw * n] when the K split exceeds one block, else nullptr
+    uint32_t *tickets;      // dense split K: kSkinnyTickets words, zero on entry and on return; the
+                            // last block of each run reduces it (no second launch); nullptr: caller reduces
     uint32_t ksplit;        // set by the launcher
     // grouped (MoE) mode; offsets == nullptr selects dense mode
     const uint32_t *offsets;  // [experts + 1] bucket offsets into `sorted`
@@ -124,6 +127,8 @@ struct SkinnyArgs {
     const uint16_t *ln_w;
     float eps;
 };
+constexpr uint32_t kSkinnyTickets = 512;        // ticket words of a split-K skinny launch (runs per slab)
+constexpr uint32_t kSkinnyMaxTicketSplit = 8;   // K slabs the in-kernel reduction takes (k <= 16384)
 hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s);
 
 // Routed MoE GEMV: one token per (expert, sorted position) pair on the m = 1

@@ -398,7 +398,10 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             if (a.partial) {  // dense split-K: [ksplit, m, nw * n], gate at f, up at n + f
                 const uint32_t nw = kGateUp ? 2 : 1;
                 float *dst = a.partial + ((size_t)slab * a.m + erow) * (size_t)(nw * crows);
-                dst[((kGateUp && ecol >= 8) ? crows : 0u) + f] = val;
+                // device-coherent store (written through, not held in this XCD's L2), so that the
+                // block reducing the run reads it without a cache write-back or invalidate
+                __hip_atomic_store(dst + ((kGateUp && ecol >= 8) ? crows : 0u) + f, val, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 if constexpr (kGateUp) {
                     float up = 0.0f;
@@ -438,6 +441,57 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         } else {
             finish(B0{}, tile_mma(B0{}), t);
         }
+    };
+
+    // ---- split K without a second launch (dense mode, a.tickets set): the ksplit blocks of a
+    // run publish their partials and take a ticket; the last one sums the run's partials in slab
+    // order (as q4_mfma_splitk_reduce_kernel does), applies the epilogue and leaves the ticket at
+    // zero.  No block waits for another.  The partials are device-coherent stores and loads, so
+    // the only ordering needed is that this block's stores have completed before its ticket
+    // (a fence would write back and invalidate whole L2s, which costs far more at this scale).
+    auto reduce_run = [&]() {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are done
+        __syncthreads();
+        uint32_t *s_ticket = reinterpret_cast<uint32_t *>(&red[0][0][0][0]);  // red is free here
+        const uint32_t rb = blockIdx.x / a.ksplit;
+        if (tid == 0) s_ticket[0] = atomicAdd(&a.tickets[rb], 1u);
+        __syncthreads();
+        if (s_ticket[0] != a.ksplit - 1) return;
+        constexpr uint32_t nw = kGateUp ? 2 : 1;
+        const uint32_t n = a.w.n;
+        const uint32_t f0 = run_begin * kTileRows, f1 = min(run_end * kTileRows, n);
+        const uint32_t nrows = f1 - f0, items = nrows * a.m;
+        const size_t stride = (size_t)a.m * nw * n;
+        for (uint32_t it = (uint32_t)tid; it < items; it += NW * 64) {
+            const uint32_t tok = it / nrows, f = f0 + it % nrows;
+            const float *p = a.partial + (size_t)tok * nw * n + f;
+            float gs[kSkinnyMaxTicketSplit], us[kSkinnyMaxTicketSplit];
+#pragma unroll
+            for (uint32_t sl = 0; sl < kSkinnyMaxTicketSplit; ++sl) {  // unconditional (clamped) loads
+                const size_t off = (size_t)min(sl, a.ksplit - 1) * stride;
+                gs[sl] = __hip_atomic_load(p + off, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                us[sl] = nw == 2 ? __hip_atomic_load(p + off + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+            }
+            float gsum = 0.0f, usum = 0.0f;
+#pragma unroll
+            for (uint32_t sl = 0; sl < kSkinnyMaxTicketSplit; ++sl) {
+                if (sl < a.ksplit) {
+                    gsum += gs[sl];
+                    usum += us[sl];
+                }
+            }
+            float val = kGateUp ? activation(gsum, a.act) * usum : gsum;
+            if (a.bias) val += bf16_to_f32(a.bias[f]);
+            const size_t o = (size_t)tok * a.ldo + f;
+            if (a.out_f32) {
+                float *out = reinterpret_cast<float *>(a.out);
+                out[o] = a.accumulate ? out[o] + val : val;
+            } else {
+                uint16_t *out = reinterpret_cast<uint16_t *>(a.out);
+                out[o] = (uint16_t)f32_to_bf16(a.accumulate ? val + bf16_to_f32(out[o]) : val);
+            }
+        }
+        if (tid == 0) __hip_atomic_store(&a.tickets[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
 
     if constexpr (!kGrouped) {  // dense: one X for the whole run
@@ -488,6 +542,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             tb = select(t);
             fetch(B0{}, 0, t - tb);
         }
+        if (a.tickets) reduce_run();
         return;
     }
 
@@ -521,7 +576,8 @@ namespace {
 template <bool GU, bool G>
 hipError_t launch_t(SkinnyArgs &a, uint32_t items, hipStream_t s) {
     // blocks per slab: every CU busy, each block a contiguous run of ceil(items / nblk) tiles
-    const uint32_t cap = std::max<uint32_t>(1, (uint32_t)tuning().skinny_max_blocks / a.ksplit);
+    uint32_t cap = std::max<uint32_t>(1, (uint32_t)tuning().skinny_max_blocks / a.ksplit);
+    if (a.tickets) cap = std::min(cap, kSkinnyTickets);  // one ticket word per run
     const uint32_t nblk = std::max<uint32_t>(1, std::min(items, cap));
     const dim3 grid(nblk * a.ksplit), block(kSkinnyWaves * 64);
     hipLaunchKernelGGL((q4_skinny_kernel<GU, G>), grid, block, 0, s, a);
@@ -543,6 +599,8 @@ hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s) {
     if (grouped && (a.nmore > 0 || a.ln_w)) return hipErrorInvalidValue;
     if (a.nmore < 0 || a.nmore > 2 || (a.nmore > 0 && (gate_up || a.partial))) return hipErrorInvalidValue;
     if (a.ln_w && a.ksplit != 1) return hipErrorInvalidValue;  // the norm needs the whole row in the slab
+    if (a.tickets && (grouped || a.nmore > 0 || !a.partial || a.ksplit < 2 || a.ksplit > kSkinnyMaxTicketSplit))
+        return hipErrorInvalidValue;
     for (int i = 0; i < a.nmore; ++i)
         if (!skinny_supported(a.more[i].w) || a.more[i].w.k != a.k) return hipErrorInvalidValue;
     const uint32_t tile_rows = gate_up ? 8 : 16;

@@ -33,6 +33,7 @@ OPT_GEMV_LONG_ROWS = 8
 OPT_GEMV_TOKENS = 9
 OPT_MOE_GEMV = 10
 OPT_GEMV_LONG_GROUPS = 11
+OPT_SPLITK_TICKETS = 12
 
 _lib = None
 
@@ -224,8 +225,9 @@ def mlp_workspace_bytes(m: int, hidden: int, intermediate: int) -> int:
 
 
 def mlp_workspace(m: int, hidden: int, intermediate: int, device="cuda") -> torch.Tensor:
-    """Device workspace of an MLP call (bf16 intermediate + split-K partials)."""
-    return torch.empty(mlp_workspace_bytes(m, hidden, intermediate), dtype=torch.uint8, device=device)
+    """Device workspace of an MLP call (bf16 intermediate, split-K partials and their counters, which
+    must start at zero: the call leaves them zero)."""
+    return torch.zeros(mlp_workspace_bytes(m, hidden, intermediate), dtype=torch.uint8, device=device)
 
 
 def qkv(q: Q4Matrix, k: Q4Matrix, v: Q4Matrix, x: torch.Tensor, q_bias=None, k_bias=None, v_bias=None,
@@ -267,7 +269,7 @@ def rmsnorm_qkv(h: torch.Tensor, ln_weight: torch.Tensor, eps: float, q: Q4Matri
 
 def rmsnorm_mlp_workspace(m: int, hidden: int, intermediate: int, device="cuda") -> torch.Tensor:
     nbytes = int(lib().kr_rmsnorm_q4_mlp_workspace_bytes(m, hidden, intermediate))
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)  # zero counters, as mlp_workspace
 
 
 def rmsnorm_mlp(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, h: torch.Tensor, ln_weight: torch.Tensor, eps: float,

@@ -321,6 +321,51 @@ def test_mlp_config1(kq, B):
     assert_rms_close(got, delta32, what=f"mlp B={B} vs f32 intermediate")
 
 
+@pytest.mark.parametrize("m", [5, 9, 16])
+def test_mlp_split_k_in_launch_reduction(kq, m):
+    """Few-token MLP: the down projection's K split (11008 = 6 slabs of 2048) reduced by the last block of
+    each run gives the bits of the separate reduction launch (same slab order); every call leaves the
+    workspace's counters at zero; graph replays give the eager bits."""
+    s = synth()
+    case(f"mlp m={m}: split-K reduced in launch vs second launch, counters, 3 graph replays")
+    g, u = s.q4_weight(11008, 2048, 1001), s.q4_weight(11008, 2048, 1002)
+    d = s.q4_weight(2048, 11008, 1003)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    h0 = s.bf16_normal((m, 2048), 1200 + m)
+    x = dev_bf16(h0)
+    ws = kq.mlp_workspace(m, 2048, 11008)
+    tickets = ws[-2048:]  # the last 512 words of the workspace
+    outs = {}
+    try:
+        for tk in (0, 1, 1):
+            kq.set_option(kq.OPT_SPLITK_TICKETS, tk)
+            h = torch.zeros((m, 2048), dtype=torch.float32, device="cuda")
+            kq.mlp(G, U, D, h, x=x, workspace=ws)
+            outs.setdefault(tk, []).append(h.cpu().numpy())
+            assert int(torch.count_nonzero(tickets)) == 0
+    finally:
+        kq.set_option(kq.OPT_SPLITK_TICKETS, 1)
+    for got in outs[1]:
+        assert np.array_equal(got.view(np.uint32), outs[0][0].view(np.uint32))
+    delta = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), h0)
+    assert_rms_close(outs[1][0], delta, what=f"mlp m={m} (in-launch split-K reduction)")
+    h = torch.zeros((m, 2048), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            kq.mlp(G, U, D, h, x=x, workspace=ws)
+    torch.cuda.synchronize()
+    for i in range(3):
+        h.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(h.cpu().numpy().view(np.uint32), outs[0][0].view(np.uint32)), f"replay {i}"
+        assert int(torch.count_nonzero(tickets)) == 0
+
+
 # ---------------------------------------------------------------- MLP (m == 1): shapes, reuse, graphs
 
 @pytest.mark.parametrize("hidden,inter", [(2048, 11008), (256, 384), (512, 1408), (1024, 4096)])
