@@ -126,17 +126,17 @@ def bench_mlp(kq, torch, synth, B, copies, steps, warmup):
 
 
 def stream_floor(kq, torch, nbytes, copies, steps, warmup):
-    """Seconds per plain read of nbytes (kr_stream_read: 16-byte non-temporal loads, nothing else) over
+    """Seconds per plain read of nbytes (kr_stream_read: one 16-byte non-temporal load per thread) over
     `copies` rotating buffers, timed like the kernels: the floor for a read of that size on this GPU."""
     n = (nbytes + 15) // 16 * 16
     gen = torch.Generator(device="cuda")
     gen.manual_seed(77)
     bufs = [torch.randint(-(2 ** 31), 2 ** 31 - 1, (n // 4,), dtype=torch.int32, device="cuda", generator=gen)
             for _ in range(copies)]
-    sink = torch.empty(int(kq.lib().kr_stream_read_sink_words(n)), dtype=torch.int32, device="cuda")
+    hits = torch.zeros(int(kq.lib().kr_stream_read_pieces(n)), dtype=torch.int32, device="cuda")
 
     def rd(i):
-        kq.stream_read(bufs[i % copies], sink)
+        kq.stream_read(bufs[i % copies], hits=hits)
 
     t = graph_time_per_step(torch, rd, copies, max(1, steps // copies), max(1, warmup // copies))
     del bufs

@@ -232,11 +232,13 @@ int kr_q4_embedding(const kr_q4_matrix *w, const uint32_t *tokens, uint32_t coun
 
 /* ---- measurement helper (no counterpart in the reference) ----
  * A plain read of `bytes` bytes of device memory, the floor the GEMV kernels are
- * compared with at the same byte count.  sink[i] = xor of the 32-bit words of
- * the i-th 16 KB of buf; sink holds kr_stream_read_sink_words(bytes) words.
- * buf 16-byte aligned, bytes a multiple of 16 (> 0). */
-size_t kr_stream_read_sink_words(size_t bytes);
-int kr_stream_read(const void *buf, size_t bytes, uint32_t *sink, void *stream);
+ * compared with at the same byte count.  hits[i] = 1 where some 16-byte unit
+ * of the i-th 1 KB of buf (the last piece may be shorter) has its four 32-bit
+ * words xor to `match`; other words of hits are not written.  hits holds
+ * kr_stream_read_pieces(bytes) words.  buf 16-byte aligned, bytes a positive
+ * multiple of 16. */
+size_t kr_stream_read_pieces(size_t bytes);
+int kr_stream_read(const void *buf, size_t bytes, uint32_t match, uint32_t *hits, void *stream);
 
 #ifdef __cplusplus
 }

@@ -292,14 +292,14 @@ int kr_get_option(int option) {
     }
 }
 
-size_t kr_stream_read_sink_words(size_t bytes) { return stream_read_sink_words(bytes); }
+size_t kr_stream_read_pieces(size_t bytes) { return stream_read_pieces(bytes); }
 
-int kr_stream_read(const void *buf, size_t bytes, uint32_t *sink, void *stream) {
-    if (!buf || !sink) return fail(KR_E_INVALID, "buf and sink must not be NULL");
+int kr_stream_read(const void *buf, size_t bytes, uint32_t match, uint32_t *hits, void *stream) {
+    if (!buf || !hits) return fail(KR_E_INVALID, "buf and hits must not be NULL");
     if (bytes == 0 || bytes % 16 != 0) return fail(KR_E_SHAPE, "bytes must be a positive multiple of 16");
-    if (!aligned(buf, 16) || !aligned(sink, 4)) return fail(KR_E_ALIGN, "buf must be 16-byte aligned, sink 4-byte");
-    if (stream_read_sink_words(bytes) > 0x7FFFFFFFu) return fail(KR_E_SHAPE, "bytes too large");
-    return hip_status(launch_stream_read(buf, bytes, sink, (hipStream_t)stream), "kr_stream_read");
+    if (!aligned(buf, 16) || !aligned(hits, 4)) return fail(KR_E_ALIGN, "buf must be 16-byte aligned, hits 4-byte");
+    if (bytes / 16 / 256 >= 0x7FFFFFFFu) return fail(KR_E_SHAPE, "bytes too large");
+    return hip_status(launch_stream_read(buf, bytes, match, hits, (hipStream_t)stream), "kr_stream_read");
 }
 
 int kr_q4_dequant(const kr_q4_matrix *w, float *out, void *stream) {

@@ -46,8 +46,8 @@ Tuning &tuning();
 constexpr uint32_t kMaxGemvK = 3 * 256 * 32;
 
 hipError_t launch_format_dequant(const Q4Mat &w, float *out, hipStream_t s);
-size_t stream_read_sink_words(size_t bytes);
-hipError_t launch_stream_read(const void *buf, size_t bytes, uint32_t *sink, hipStream_t s);
+size_t stream_read_pieces(size_t bytes);
+hipError_t launch_stream_read(const void *buf, size_t bytes, uint32_t match, uint32_t *hits, hipStream_t s);
 hipError_t launch_from_blocks36(const void *blocks, uint32_t n, uint32_t k, uint32_t *qw, uint16_t *sc,
                                 uint16_t *bi, hipStream_t s);
 hipError_t launch_to_blocks36(const Q4Mat &w, void *blocks, hipStream_t s);

@@ -68,8 +68,8 @@ def lib():
             "kr_set_option": (i32, [i32, i32]),
             "kr_get_option": (i32, [i32]),
             "kr_q4_dequant": (i32, [M, vp, vp]),
-            "kr_stream_read_sink_words": (sz, [sz]),
-            "kr_stream_read": (i32, [vp, sz, vp, vp]),
+            "kr_stream_read_pieces": (sz, [sz]),
+            "kr_stream_read": (i32, [vp, sz, u32, vp, vp]),
             "kr_q4_from_blocks36": (i32, [vp, u32, u32, vp, vp, vp, vp]),
             "kr_q4_to_blocks36": (i32, [M, vp, vp]),
             "kr_f16_to_bf16": (i32, [vp, vp, sz, vp]),
@@ -408,15 +408,16 @@ def argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None
     return out
 
 
-def stream_read(buf: torch.Tensor, sink: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
-    """Measurement helper (no reference counterpart): a plain read of buf's bytes.
-    sink[i] (int32) = xor of the 32-bit words of the i-th 16 KB of buf."""
+def stream_read(buf: torch.Tensor, match: int = 0x9E3779B9, hits: Optional[torch.Tensor] = None,
+                stream=None) -> torch.Tensor:
+    """Measurement helper (no reference counterpart): a plain read of buf's bytes.  hits[i] (int32) is set
+    to 1 where some 16-byte unit of the i-th 1 KB of buf xors (four 32-bit words) to `match` (others
+    untouched)."""
     nbytes = buf.numel() * buf.element_size()
-    words = int(lib().kr_stream_read_sink_words(nbytes))
-    if sink is None:
-        sink = torch.empty(words, dtype=torch.int32, device=buf.device)
-    _check(lib().kr_stream_read(_ptr(buf), nbytes, _ptr(sink), _stream(stream)))
-    return sink
+    if hits is None:
+        hits = torch.zeros(int(lib().kr_stream_read_pieces(nbytes)), dtype=torch.int32, device=buf.device)
+    _check(lib().kr_stream_read(_ptr(buf), nbytes, match & 0xFFFFFFFF, _ptr(hits), _stream(stream)))
+    return hits
 
 
 # ---- names of the reference operator surface (encoder.rs) -------------------------------

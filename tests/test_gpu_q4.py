@@ -160,17 +160,23 @@ def test_gemv_long_row_kernel_options(kq, n, k):
         assert np.array_equal(y.view(np.uint32), outs[(2, 8)].view(np.uint32)), key
 
 
-def test_stream_read_xor_per_block(kq):
-    """The streaming-floor helper reads every byte: sink[i] = xor of the words of the i-th 16 KB."""
-    case("stream_read 3 x 16 KB + 48 B")
+def test_stream_read_reads_every_piece(kq):
+    """The streaming-floor helper reads every byte: hits[i] = 1 exactly for the 1 KB pieces holding a
+    16-byte unit whose four words xor to `match` (a ragged last piece included)."""
+    case("stream_read 37 x 1 KB + 48 B, three planted units")
     rng = np.random.default_rng(5)
-    words = rng.integers(0, 2 ** 32, size=(3 * 16384 + 48) // 4, dtype=np.uint32)
+    words = rng.integers(0, 2 ** 32, size=(37 * 1024 + 48) // 4, dtype=np.uint32)
+    match = 0x2545F491
+    for unit in (3, 20 * 64 + 63, 37 * 64 + 2):  # make these units xor to `match` through their first word
+        u = words[4 * unit:4 * unit + 4]
+        u[0] ^= np.bitwise_xor.reduce(u) ^ np.uint32(match)
+    unit_hit = np.bitwise_xor.reduce(words.reshape(-1, 4), axis=1) == np.uint32(match)
+    want = np.zeros(38, dtype=bool)
+    np.logical_or.at(want, np.arange(unit_hit.size) // 64, unit_hit)
     buf = torch.from_numpy(words.view(np.int32)).cuda()
-    sink = kq.stream_read(buf).cpu().numpy().view(np.uint32)
-    per = 16384 // 4
-    want = [np.bitwise_xor.reduce(words[i:i + per]) for i in range(0, words.size, per)]
-    assert sink.size == len(want) == 4
-    assert np.array_equal(sink, np.array(want, dtype=np.uint32))
+    hits = kq.stream_read(buf, match=match).cpu().numpy()
+    assert hits.size == 38
+    assert np.array_equal(hits != 0, want) and hits[[0, 20, 37]].all()
     with pytest.raises(kq.KrError):
         kq.stream_read(buf[:3])  # 12 bytes: not a multiple of 16
 
