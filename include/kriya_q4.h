@@ -164,8 +164,10 @@ int kr_q4_qkv(const kr_q4_matrix *q, const kr_q4_matrix *k, const kr_q4_matrix *
  * kr_q4_mlp_workspace_bytes(m, gate->k, gate->n), 16-byte aligned; calls that
  * share a workspace must not overlap in time.  For m > 1 the workspace also
  * holds split-K partial sums of the down projection, reduced in a fixed order,
- * and the counters that pick the block that reduces them: zero-fill the
- * workspace once before its first use (every call leaves them zero). */
+ * and the counters that pick the block that reduces them (at its start, the
+ * same place for every m): zero-fill the workspace once before its first use
+ * (every call leaves them zero); a workspace sized for the largest m serves
+ * every smaller one. */
 size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermediate);
 int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down,
               const uint16_t *x, void *h, int h_dtype, uint32_t m, int activation,

@@ -437,17 +437,24 @@ int kr_q4_qkv(const kr_q4_matrix *q, const kr_q4_matrix *k, const kr_q4_matrix *
     return hip_status(launch_mfma(args, bm_class(m), s), "kr_q4_qkv");
 }
 
+// MLP workspace layout: the tickets of the in-launch split-K reduction first, at the same place for
+// every m (zero between calls, so a workspace can serve several m), then the bf16 activation
+// [m, inter], then (m > 1) the f32 split-K partials of the down projection.
+constexpr size_t kMlpTicketBytes = ((size_t)kSkinnyTickets * 4 + 255) / 256 * 256;
+static uint32_t *mlp_ws_tickets(void *ws) { return (uint32_t *)ws; }
+static uint16_t *mlp_ws_act(void *ws) { return (uint16_t *)((char *)ws + kMlpTicketBytes); }
+static float *mlp_ws_partial(void *ws, uint32_t m, uint32_t inter) {
+    return (float *)((char *)ws + kMlpTicketBytes + round_up((size_t)m * inter * 2, 256));
+}
+
 size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermediate) {
-    size_t bytes = round_up((size_t)m * intermediate * 2, 256);
-    if (m > 1) {
-        bytes += partial_bytes(m, hidden, intermediate, 1);  // split-K partials of the down projection
-        bytes += round_up((size_t)kSkinnyTickets * 4, 256);   // and its tickets (zero between calls)
-    }
+    size_t bytes = kMlpTicketBytes + round_up((size_t)m * intermediate * 2, 256);
+    if (m > 1) bytes += partial_bytes(m, hidden, intermediate, 1);  // split-K partials of the down projection
     return bytes;
 }
 
 // The MLP's down projection, accumulated into h, after the activation `act` (bf16 [m, inter]) was
-// written to the start of `workspace` (kr_q4_mlp_workspace_bytes layout: act, then split-K partials).
+// written to the workspace (layout above).
 static int mlp_down(const kr_q4_matrix *gate, const kr_q4_matrix *down, const uint16_t *act, void *h, int h_dtype,
                     uint32_t m, void *workspace, void *stream) {
     if (m == 1 || (tuning().gemv_tokens && gemv_tokens_supported(m, gate->k, true) &&
@@ -455,8 +462,8 @@ static int mlp_down(const kr_q4_matrix *gate, const kr_q4_matrix *down, const ui
         return kr_q4_linear(down, act, m, h, h_dtype, 1, stream);
     // down projection: few N tiles at small m, so K is split over blocks; partials (and the
     // tickets of the in-launch reduction) live in the workspace
-    float *partial = (float *)((char *)workspace + round_up((size_t)m * gate->n * 2, 256));
-    uint32_t *tickets = (uint32_t *)((char *)partial + partial_bytes(m, gate->k, gate->n, 1));
+    float *partial = mlp_ws_partial(workspace, m, gate->n);
+    uint32_t *tickets = mlp_ws_tickets(workspace);
     if (skinny_fits(m, to_mat(down), true))
         return hip_status(run_skinny(to_mat(down), nullptr, act, m, h, nullptr, down->n, h_dtype, 1, 0, partial,
                                      (hipStream_t)stream, nullptr, 0.0f, tickets),
@@ -492,7 +499,7 @@ int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matr
     if (!workspace || workspace_bytes < need)
         return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
     if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
-    uint16_t *act = (uint16_t *)workspace;
+    uint16_t *act = mlp_ws_act(workspace);
     if (int rc = kr_q4_gate_up_act(gate, up, x, m, act, KR_DTYPE_BF16, activation, stream)) return rc;
     return mlp_down(gate, down, act, h, h_dtype, m, workspace, stream);
 }
@@ -757,7 +764,7 @@ int kr_rmsnorm_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
     const size_t mlp_bytes = kr_q4_mlp_workspace_bytes(m, gate->k, gate->n);
     if (m == 1 && gemv_batch_supported(gate->k)) {
         // gate/up with the norm fused into the x load, then the accumulating down projection
-        uint16_t *act = (uint16_t *)workspace;
+        uint16_t *act = mlp_ws_act(workspace);
         const Q4Mat g = to_mat(gate), u = to_mat(up);
         void *outs[1] = {act};
         const uint16_t *biases[1] = {nullptr};
@@ -769,7 +776,7 @@ int kr_rmsnorm_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
     const bool tokens = tuning().gemv_tokens && gemv_tokens_supported(m, gate->k, true);
     if (!tokens && skinny_fits(m, to_mat(gate), false) && skinny_supported(to_mat(up))) {
         // few tokens on the matrix cores: the norm is applied while gate/up stages x
-        uint16_t *act = (uint16_t *)workspace;
+        uint16_t *act = mlp_ws_act(workspace);
         const Q4Mat g = to_mat(gate), u = to_mat(up);
         if (int rc = hip_status(run_skinny(g, &u, h, m, act, nullptr, gate->n, KR_DTYPE_BF16, 0, activation, nullptr, s,
                                            ln_weight, eps),

@@ -340,7 +340,7 @@ def test_mlp_split_k_in_launch_reduction(kq, m):
     h0 = s.bf16_normal((m, 2048), 1200 + m)
     x = dev_bf16(h0)
     ws = kq.mlp_workspace(m, 2048, 11008)
-    tickets = ws[-2048:]  # the last 512 words of the workspace
+    tickets = ws[:2048]  # the first 512 words of the workspace
     outs = {}
     try:
         for tk in (0, 1, 1):
@@ -353,6 +353,13 @@ def test_mlp_split_k_in_launch_reduction(kq, m):
         kq.set_option(kq.OPT_SPLITK_TICKETS, 1)
     for got in outs[1]:
         assert np.array_equal(got.view(np.uint32), outs[0][0].view(np.uint32))
+    # a workspace sized for 16 rows serves smaller m too (the counters sit at the same place for every m)
+    big = kq.mlp_workspace(16, 2048, 11008)
+    for mm in (16, m):
+        hh = torch.zeros((mm, 2048), dtype=torch.float32, device="cuda")
+        kq.mlp(G, U, D, hh, x=x[:mm] if mm <= m else dev_bf16(s.bf16_normal((mm, 2048), 1300)), workspace=big)
+        assert int(torch.count_nonzero(big[:2048])) == 0
+    assert np.array_equal(hh.cpu().numpy().view(np.uint32), outs[0][0].view(np.uint32))
     delta = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), h0)
     assert_rms_close(outs[1][0], delta, what=f"mlp m={m} (in-launch split-K reduction)")
     h = torch.zeros((m, 2048), dtype=torch.float32, device="cuda")
