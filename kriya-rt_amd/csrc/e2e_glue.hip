@@ -596,12 +596,18 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *logits, uint3
         }
     };
     if (n % 4 == 0) {
+        // Per float4 a cheap max first (fmaxf drops NaN); only a quad that can win is searched
+        // for its first lane holding that max -- the order of `take` within the quad.
         const f32x4 *r4 = reinterpret_cast<const f32x4 *>(row);
 #pragma unroll 8
         for (uint32_t i = tid; i < n / 4; i += 1024) {
             const f32x4 x = r4[i];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) take(x[c], 4 * i + c);
+            const float m = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+            if (m > v || (idx == 0xFFFFFFFFu && m == m)) {
+                const uint32_t c = x[0] == m ? 0u : x[1] == m ? 1u : x[2] == m ? 2u : 3u;
+                v = m;
+                idx = 4 * i + c;
+            }
         }
     } else {
         for (uint32_t i = tid; i < n; i += 1024) take(row[i], i);

@@ -190,6 +190,33 @@ def test_argmax_ties_and_nan(kq):
     assert got.tolist() == [int(np.argmax(x[0])), 10, 999, 123]
 
 
+def _argmax_ref(row):
+    """Lowest index of the largest non-NaN value; 0 when every value is NaN."""
+    valid = ~np.isnan(row)
+    if not valid.any():
+        return 0
+    return int(np.flatnonzero(valid & (row == row[valid].max()))[0])
+
+
+@pytest.mark.parametrize("n", [151936, 1001, 8])
+def test_argmax_quads_and_vocab_rows(kq, n):
+    case(f"argmax n={n}: ties inside and across float4 quads, NaN next to the max, -inf rows")
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal((8, n)).astype(np.float32)
+    x[1, 5] = x[1, 6] = 60.0                          # tie inside one quad
+    x[2, n - 1] = x[2, n // 2] = 60.0                 # tie across quads / threads
+    x[3, 0:4] = [np.nan, 60.0, np.nan, 60.0]          # NaN beside the max in its quad
+    x[4, :] = -np.inf
+    x[5, :] = np.nan
+    x[5, n - 2:] = [-np.inf, -np.inf]                 # only -inf besides NaN: the first -inf
+    x[6, :] = -np.inf
+    x[6, 3] = np.nan
+    x[7, n - 1] = np.inf
+    got = kq.argmax(torch.from_numpy(x).cuda()).cpu().numpy()
+    want = [_argmax_ref(r) for r in x]
+    assert got.tolist() == want
+
+
 def decode_ref(m, cfg, tokens, pos):
     """CPU restatement of one decode step (qwen_decode.QwenQ4Decoder.step)."""
     B = len(tokens)
