@@ -598,15 +598,26 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *logits, uint3
     if (n % 4 == 0) {
         // Per float4 a cheap max first (fmaxf drops NaN); only a quad that can win is searched
         // for its first lane holding that max -- the order of `take` within the quad.
+        // Eight quads are requested before any is scanned (clamped, unconditional loads): with a
+        // load per scan step the branch keeps the compiler from hoisting the next loads, and each
+        // quad costs a round trip.
         const f32x4 *r4 = reinterpret_cast<const f32x4 *>(row);
-#pragma unroll 8
-        for (uint32_t i = tid; i < n / 4; i += 1024) {
-            const f32x4 x = r4[i];
-            const float m = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-            if (m > v || (idx == 0xFFFFFFFFu && m == m)) {
-                const uint32_t c = x[0] == m ? 0u : x[1] == m ? 1u : x[2] == m ? 2u : 3u;
-                v = m;
-                idx = 4 * i + c;
+        const uint32_t n4 = n / 4;
+        constexpr uint32_t kBatch = 8;
+        for (uint32_t i0 = tid; i0 < n4; i0 += 1024 * kBatch) {
+            f32x4 xq[kBatch];
+#pragma unroll
+            for (uint32_t j = 0; j < kBatch; ++j) xq[j] = r4[min(i0 + 1024 * j, n4 - 1)];
+#pragma unroll
+            for (uint32_t j = 0; j < kBatch; ++j) {
+                const uint32_t i = i0 + 1024 * j;
+                const f32x4 x = xq[j];
+                const float m = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+                if (i < n4 && (m > v || (idx == 0xFFFFFFFFu && m == m))) {
+                    const uint32_t c = x[0] == m ? 0u : x[1] == m ? 1u : x[2] == m ? 2u : 3u;
+                    v = m;
+                    idx = 4 * i + c;
+                }
             }
         }
     } else {
