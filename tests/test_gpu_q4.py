@@ -379,6 +379,46 @@ def test_mlp_split_k_in_launch_reduction(kq, m):
         assert int(torch.count_nonzero(tickets)) == 0
 
 
+@pytest.mark.parametrize("m,inter", [(9, 16384), (12, 20480)])
+def test_mlp_split_k_edges(kq, m, inter):
+    """The down projection's K split at its edges: 16384 = 8 slabs (the most the in-launch reduction takes)
+    and 20480 = 10 slabs (reduced by a second launch); both against the oracle, and option on/off give the
+    same bits."""
+    s = synth()
+    case(f"mlp m={m} hidden=512 inter={inter}: split-K edges")
+    g, u = s.q4_weight(inter, 512, 1401), s.q4_weight(inter, 512, 1402)
+    d = s.q4_weight(512, inter, 1403)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    h0 = s.bf16_normal((m, 512), 1404)
+    x = dev_bf16(h0)
+    ws = kq.mlp_workspace(m, 512, inter)
+    outs = []
+    try:
+        for tk in (1, 0):
+            kq.set_option(kq.OPT_SPLITK_TICKETS, tk)
+            h = torch.zeros((m, 512), dtype=torch.float32, device="cuda")
+            kq.mlp(G, U, D, h, x=x, workspace=ws)
+            outs.append(h.cpu().numpy())
+            assert int(torch.count_nonzero(ws[:2048])) == 0
+    finally:
+        kq.set_option(kq.OPT_SPLITK_TICKETS, 1)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    delta = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), h0)
+    assert_rms_close(outs[0], delta, what=f"mlp m={m} inter={inter}")
+
+
+@pytest.mark.parametrize("m", [1, 3, 16])
+def test_linear_at_the_k_limit(kq, m):
+    """k = 24576, the documented maximum: the m = 1 split-K block kernel, the token GEMV and the few-token
+    kernel (12 slabs, through the MFMA path's workspace-free fallback or its own split) against the oracle."""
+    s = synth()
+    case(f"q4_linear m={m} n=96 k=24576")
+    wq = s.q4_weight(96, 24576, 1500 + m)
+    x = s.bf16_normal((m, 24576), 1501)
+    y = kq.q4_linear(q4_dev(kq, wq), dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy()
+    assert_rms_close(y, O.q4_matmul(O.Q4Planar(*wq), x), what=f"k limit m={m}")
+
+
 # ---------------------------------------------------------------- MLP (m == 1): shapes, reuse, graphs
 
 @pytest.mark.parametrize("hidden,inter", [(2048, 11008), (256, 384), (512, 1408), (1024, 4096)])
