@@ -114,6 +114,19 @@ int kr_q4_from_blocks36(const void *blocks, uint32_t n, uint32_t k,
 /* Planar triplet -> 36-byte blocks (inverse of the above, byte-identical). */
 int kr_q4_to_blocks36(const kr_q4_matrix *w, void *blocks, void *stream);
 
+/* Split planes (tensor.rs:117-211: ScaledAlignedQ4Block [n * k/64] of 32
+ * nibble bytes, 16-byte aligned, and BlockQ4ScaleBias [n * k/64] {scale_bf16,
+ * bias_bf16}; block (r, g) at index r*(k/64)+g, the layout split_slice makes for
+ * the consolidated QKV, encoder.rs:998-1015) -> planar triplet.  The nibble
+ * plane holds the planar qw bytes unchanged, so qw may equal qs (then only the
+ * pairs are split); otherwise it is copied.  qs, qw 16-byte aligned, sb 4-byte.
+ * Replaces BlockQ4Group64::from_split (tensor.rs:172-187) feeding a planar bind. */
+int kr_q4_from_split(const void *qs, const void *sb, uint32_t n, uint32_t k,
+                     uint32_t *qw, uint16_t *scales, uint16_t *biases, void *stream);
+/* Planar triplet -> split planes (inverse of the above; qs may equal w->qw).
+ * Replaces BlockQ4Group64::split_slice (tensor.rs:156-170). */
+int kr_q4_to_split(const kr_q4_matrix *w, void *qs, void *sb, void *stream);
+
 /* MLX scale/bias planes stored as IEEE half -> bf16 bits, element-wise:
  * bf16_rne(f16_to_f32(h)).  Replaces parse_half_endian(is_f16 = true)
  * (safetensors_loader.rs:310-318; quantizer.rs:19-57).  in may equal out. */

@@ -327,6 +327,24 @@ int kr_q4_to_blocks36(const kr_q4_matrix *w, void *blocks, void *stream) {
     return hip_status(launch_to_blocks36(to_mat(w), blocks, (hipStream_t)stream), "kr_q4_to_blocks36");
 }
 
+int kr_q4_from_split(const void *qs, const void *sb, uint32_t n, uint32_t k, uint32_t *qw, uint16_t *scales,
+                     uint16_t *biases, void *stream) {
+    if (!qs || !sb || !qw || !scales || !biases) return fail(KR_E_INVALID, "NULL pointer");
+    if (k == 0 || k % 64 != 0) return fail(KR_E_SHAPE, "k=%u is not a positive multiple of 64", k);
+    if (!aligned(qs, 16) || !aligned(qw, 16)) return fail(KR_E_ALIGN, "qs and qw must be 16-byte aligned");
+    if (!aligned(sb, 4)) return fail(KR_E_ALIGN, "sb must be 4-byte aligned");
+    if (!aligned(scales, 2) || !aligned(biases, 2)) return fail(KR_E_ALIGN, "scales/biases must be 2-byte aligned");
+    return hip_status(launch_from_split(qs, sb, n, k, qw, scales, biases, (hipStream_t)stream), "kr_q4_from_split");
+}
+
+int kr_q4_to_split(const kr_q4_matrix *w, void *qs, void *sb, void *stream) {
+    if (int rc = check_matrix(w, "w")) return rc;
+    if (!qs || !sb) return fail(KR_E_INVALID, "qs and sb must not be NULL");
+    if (!aligned(qs, 16)) return fail(KR_E_ALIGN, "qs must be 16-byte aligned");
+    if (!aligned(sb, 4)) return fail(KR_E_ALIGN, "sb must be 4-byte aligned");
+    return hip_status(launch_to_split(to_mat(w), qs, sb, (hipStream_t)stream), "kr_q4_to_split");
+}
+
 int kr_f16_to_bf16(const uint16_t *in, uint16_t *out, size_t count, void *stream) {
     if (count == 0) return ok();
     if (!in || !out) return fail(KR_E_INVALID, "NULL pointer");

@@ -51,6 +51,9 @@ hipError_t launch_stream_read(const void *buf, size_t bytes, uint32_t match, uin
 hipError_t launch_from_blocks36(const void *blocks, uint32_t n, uint32_t k, uint32_t *qw, uint16_t *sc,
                                 uint16_t *bi, hipStream_t s);
 hipError_t launch_to_blocks36(const Q4Mat &w, void *blocks, hipStream_t s);
+hipError_t launch_from_split(const void *qs, const void *sb, uint32_t n, uint32_t k, uint32_t *qw, uint16_t *sc,
+                             uint16_t *bi, hipStream_t s);
+hipError_t launch_to_split(const Q4Mat &w, void *qs, void *sb, hipStream_t s);
 hipError_t launch_f16_to_bf16(const uint16_t *in, uint16_t *out, size_t count, hipStream_t s);
 
 // ---- batched (m > 1) matrix-core path (q4_mfma.hip)

@@ -4,6 +4,8 @@
 //   dequantize_q4_group64_to_f32   crates/kriya-core/src/quantizer.rs:112-126
 //   BlockQ4Group64 layout          crates/kriya-core/src/tensor.rs:104-115
 //   MLX triplet repack             crates/kriya-core/src/safetensors_loader.rs:221-273
+//   split planes (ScaledAlignedQ4Block + BlockQ4ScaleBias)
+//                                  crates/kriya-core/src/tensor.rs:117-211
 //   parse_half_endian              crates/kriya-core/src/safetensors_loader.rs:310-318
 //
 // All three are HBM-bound byte movers; each thread moves one 16- or 36-byte
@@ -69,6 +71,38 @@ __global__ __launch_bounds__(256) void to_blocks36_kernel(Q4Mat w, uint32_t *__r
     blk[5] = b.x; blk[6] = b.y; blk[7] = b.z; blk[8] = b.w;
 }
 
+// Split planes (tensor.rs:117-211): block i's 32 nibble bytes are 16-byte
+// aligned at qs + 32 i -- the same bytes, in the same order, as the 8 planar
+// words of group g of row r (i = r * G + g) -- and its {scale, bias} bf16 pair
+// is the u32 sb[i] = scale | bias << 16.  One thread per block.  With qw == qs
+// the nibbles are left in place and only the pairs are split.
+__global__ __launch_bounds__(256) void from_split_kernel(const u32x4 *qs, const uint32_t *__restrict__ sb,
+                                                         size_t nblocks, u32x4 *qw, uint16_t *__restrict__ sc,
+                                                         uint16_t *__restrict__ bi) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    const uint32_t p = sb[i];
+    sc[i] = (uint16_t)(p & 0xFFFFu);
+    bi[i] = (uint16_t)(p >> 16);
+    if (qw != qs) {
+        const u32x4 a = qs[2 * i], b = qs[2 * i + 1];
+        qw[2 * i] = a;
+        qw[2 * i + 1] = b;
+    }
+}
+
+__global__ __launch_bounds__(256) void to_split_kernel(Q4Mat w, u32x4 *qs, uint32_t *__restrict__ sb, size_t nblocks) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nblocks) return;
+    sb[i] = (uint32_t)w.sc[i] | ((uint32_t)w.bi[i] << 16);
+    const u32x4 *q = reinterpret_cast<const u32x4 *>(w.qw);
+    if (qs != q) {
+        const u32x4 a = q[2 * i], b = q[2 * i + 1];
+        qs[2 * i] = a;
+        qs[2 * i + 1] = b;
+    }
+}
+
 // quantizer.rs:31-57 restated on bits (subnormal renormalisation by shifting,
 // inf/NaN payload kept), then the RNE of quantizer.rs:19-24.
 __device__ __forceinline__ uint32_t f16_bits_to_f32_bits(uint32_t h) {
@@ -114,6 +148,23 @@ hipError_t launch_to_blocks36(const Q4Mat &w, void *blocks, hipStream_t s) {
     if (nb == 0) return hipSuccess;
     hipLaunchKernelGGL(to_blocks36_kernel, grid_for(nb), dim3(256), 0, s, w, reinterpret_cast<uint32_t *>(blocks),
                        nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_from_split(const void *qs, const void *sb, uint32_t n, uint32_t k, uint32_t *qw, uint16_t *sc,
+                             uint16_t *bi, hipStream_t s) {
+    const size_t nb = (size_t)n * (k >> 6);
+    if (nb == 0) return hipSuccess;
+    hipLaunchKernelGGL(from_split_kernel, grid_for(nb), dim3(256), 0, s, reinterpret_cast<const u32x4 *>(qs),
+                       reinterpret_cast<const uint32_t *>(sb), nb, reinterpret_cast<u32x4 *>(qw), sc, bi);
+    return hipGetLastError();
+}
+
+hipError_t launch_to_split(const Q4Mat &w, void *qs, void *sb, hipStream_t s) {
+    const size_t nb = (size_t)w.n * (w.k >> 6);
+    if (nb == 0) return hipSuccess;
+    hipLaunchKernelGGL(to_split_kernel, grid_for(nb), dim3(256), 0, s, w, reinterpret_cast<u32x4 *>(qs),
+                       reinterpret_cast<uint32_t *>(sb), nb);
     return hipGetLastError();
 }
 

@@ -72,6 +72,8 @@ def lib():
             "kr_stream_read": (i32, [vp, sz, u32, vp, vp]),
             "kr_q4_from_blocks36": (i32, [vp, u32, u32, vp, vp, vp, vp]),
             "kr_q4_to_blocks36": (i32, [M, vp, vp]),
+            "kr_q4_from_split": (i32, [vp, vp, u32, u32, vp, vp, vp, vp]),
+            "kr_q4_to_split": (i32, [M, vp, vp, vp]),
             "kr_f16_to_bf16": (i32, [vp, vp, sz, vp]),
             "kr_q4_linear": (i32, [M, vp, u32, vp, i32, i32, vp]),
             "kr_q4_gate_up_act": (i32, [M, M, vp, u32, vp, i32, i32, vp]),
@@ -164,6 +166,26 @@ class Q4Matrix:
         out = torch.empty(self.n * (self.k // 64) * 36, dtype=torch.uint8, device=self.qw.device)
         _check(lib().kr_q4_to_blocks36(ctypes.byref(self._desc), _ptr(out), _stream(stream)))
         return out
+
+    @classmethod
+    def from_split(cls, qs: torch.Tensor, sb: torch.Tensor, n: int, k: int, in_place: bool = False,
+                   stream=None) -> "Q4Matrix":
+        """Split planes (32-byte nibble blocks, {scale, bias} bf16 pairs; uint8 device tensors) -> planar.
+        in_place: the nibble plane becomes qw itself (no copy)."""
+        w = cls.empty(n, k, device=qs.device)
+        if in_place:
+            w = cls(qs.view(torch.int32).view(n, k // 8), w.scales, w.biases)
+        _check(lib().kr_q4_from_split(_ptr(qs), _ptr(sb), n, k, _ptr(w.qw), _ptr(w.scales), _ptr(w.biases),
+                                      _stream(stream)))
+        return w
+
+    def to_split(self, stream=None):
+        """Planar -> (nibble plane, {scale, bias} plane) as uint8 device tensors."""
+        nb = self.n * (self.k // 64)
+        qs = torch.empty(nb * 32, dtype=torch.uint8, device=self.qw.device)
+        sb = torch.empty(nb * 4, dtype=torch.uint8, device=self.qw.device)
+        _check(lib().kr_q4_to_split(ctypes.byref(self._desc), _ptr(qs), _ptr(sb), _stream(stream)))
+        return qs, sb
 
     def rows(self, lo: int, hi: int) -> "Q4Matrix":
         return Q4Matrix(self.qw[lo:hi], self.scales[lo:hi], self.biases[lo:hi])

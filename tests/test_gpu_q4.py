@@ -70,6 +70,29 @@ def test_blocks36_round_trip_on_gpu(kq):
     assert np.array_equal(back, lcg)
 
 
+def test_split_planes_on_gpu(kq):
+    """Split planes (tensor.rs:117-211) -> planar on the GPU: bit-equal to the 36-byte path and to the
+    oracle's split (pinned by the reference's split/rejoin KATs), copied or in place; planar -> split
+    gives the oracle's planes back."""
+    case("split planes <-> planar, 1000 LCG blocks (8 x 125 groups)")
+    lcg = np.array(KATS["lcg_blocks_1000"], np.uint8)
+    n, k = 8, 125 * 64
+    qs, sb = O.split_blocks36(lcg)
+    ref = kq.Q4Matrix.from_blocks36(torch.from_numpy(lcg.ravel().copy()).cuda(), n, k)
+    for in_place in (False, True):
+        qs_dev = torch.from_numpy(qs.ravel().copy()).cuda()
+        sb_dev = torch.from_numpy(sb.view(np.uint8).ravel().copy()).cuda()
+        w = kq.Q4Matrix.from_split(qs_dev, sb_dev, n, k, in_place=in_place)
+        assert (w.qw.data_ptr() == qs_dev.data_ptr()) == in_place
+        for a, b in ((w.qw, ref.qw), (w.scales, ref.scales), (w.biases, ref.biases)):
+            assert torch.equal(a, b), f"in_place={in_place}"
+    qs2, sb2 = ref.to_split()
+    assert np.array_equal(qs2.cpu().numpy(), qs.ravel())
+    assert np.array_equal(sb2.cpu().numpy().view(np.uint16), sb.ravel())
+    with pytest.raises(kq.KrError):
+        kq.Q4Matrix.from_split(qs_dev, sb_dev, n, 100)  # k not a multiple of 64
+
+
 def test_blocks36_config0_planar_equivalence(kq):
     case("cfg0 planar -> blocks36 (oracle) -> planar (gpu)")
     wq = synth().q4_weight(11008, 2048, 0)
