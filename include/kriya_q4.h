@@ -221,7 +221,10 @@ int kr_moe_scan_scatter(const uint32_t *selected, uint32_t num_assign, uint32_t 
  * For each assignment a = t * topk + k with expert e:
  *   h_a = bf16(act(gate_e . x_t) * (up_e . x_t)),   d_a = down_e . h_a  (f32),
  *   y[t] = sum over k = 0 .. topk-1 of fma(weights[a], d_a, acc), in slot order,
- * stored as y_dtype; accumulate = 1 adds it to y as kr_q4_linear does.
+ * stored as y_dtype; accumulate = 1 adds it to y as kr_q4_linear does.  A
+ * shared expert (moe_combine_routed_and_shared_bf16 with has_shared_expert,
+ * transformer_glue.metal:394-400) is this form with y holding the shared
+ * expert's bf16 output: the routed sum, then + shared, rounded once to bf16.
  * offsets and sorted_assign are kr_moe_route's.  Every expert's weights are read
  * once per call for all the tokens routed to it (grouped matmul; the reference
  * re-reads them per routed token).  The reference also rounds gate.x, up.x and
