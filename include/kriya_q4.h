@@ -223,7 +223,7 @@ int kr_moe_scan_scatter(const uint32_t *selected, uint32_t num_assign, uint32_t 
  *   y[t] = sum over k = 0 .. topk-1 of fma(weights[a], d_a, acc), in slot order,
  * stored as y_dtype; accumulate = 1 adds it to y as kr_q4_linear does.  A
  * shared expert (moe_combine_routed_and_shared_bf16 with has_shared_expert,
- * transformer_glue.metal:394-400) is this form with y holding the shared
+ * transformer_glue.metal:396-398) is this form with y holding the shared
  * expert's bf16 output: the routed sum, then + shared, rounded once to bf16.
  * offsets and sorted_assign are kr_moe_route's.  Every expert's weights are read
  * once per call for all the tokens routed to it (grouped matmul; the reference
