@@ -289,7 +289,11 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
                                                               uint32_t q_heads, uint32_t kv_heads, uint32_t D,
                                                               uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx,
                                                               float *part) {
-    __shared__ __align__(16) float qs[GP * kGlueMaxHeadDim];  // rotated q [G][D]
+    // rotated q [G][D]; after the scores, the value tile [kSplitLen][D] bf16 in the same memory
+    constexpr uint32_t kQsFloats = GP * kGlueMaxHeadDim > kSplitLen * kGlueMaxHeadDim / 2
+                                       ? GP * kGlueMaxHeadDim
+                                       : kSplitLen * kGlueMaxHeadDim / 2;
+    __shared__ __align__(16) float qs[kQsFloats];
     __shared__ float sc[GP][kSplitLen];                        // scores, then exp(score - m)
     __shared__ __align__(16) float knew[kGlueMaxHeadDim];
     __shared__ __align__(16) uint16_t vnew[kGlueMaxHeadDim];
@@ -437,7 +441,24 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
         if (writer && g < G) sc[g][r] = p0 + r < p1 ? dot[0] * (1.0f / sqrtf((float)D)) : -INFINITY;
     }
     __syncthreads();
-    // 4. per head: row r takes head r, lane c position p0 + c
+    // 4a. the value tile into LDS, over q's rows (read only by the scores, done): row c =
+    //     position p0 + c, the 8 dims of piece r [+16]; zero past the sequence (vw), the new
+    //     value at the new position
+    uint16_t *vt = reinterpret_cast<uint16_t *>(qs);
+    {
+        const bool vfresh = has_new && p0 + c == pos;
+#pragma unroll
+        for (uint32_t j = 0; j < 2; ++j) {
+            const uint32_t pc = r + 16 * j;
+            if (16 * j >= P) break;  // uniform: rows of D <= 128 need one round
+            if (pc < P) {
+                u32x4 w = vw[j];
+                if (vfresh) w = *reinterpret_cast<const u32x4 *>(&vnew[8 * pc]);
+                *reinterpret_cast<u32x4 *>(&vt[c * D + 8 * pc]) = w;
+            }
+        }
+    }
+    // 4b. per head: row r takes head r, lane c position p0 + c
     float m_keep = 0.0f, l_keep = 0.0f;
     if (r < G) {
         const float x = sc[r][c];
@@ -453,39 +474,25 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
         l_keep = l;
     }
     __syncthreads();
-    // 5. values: lane c (position p0 + c) of row r (piece r [+16]) for the G heads
-    const bool vfresh = has_new && p0 + c == pos;
-    float pr[GP];
+    // 5. values: thread (head g, dims 4 d4 .. + 3) sums its 16 positions in order from the LDS
+    //    tile -- no cross-lane reduction (positions past the sequence have weight 0 and zero
+    //    values)
+    const uint32_t D4 = D / 4;
+    for (uint32_t it = tid; it < G * D4; it += 256) {
+        const uint32_t g = it / D4, d = 4 * (it % D4);
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
 #pragma unroll
-    for (int g = 0; g < GP; ++g) pr[g] = ((uint32_t)g < G && p0 + c < p1) ? sc[g][c] : 0.0f;
-#pragma unroll
-    for (uint32_t j = 0; j < 2; ++j) {
-        const uint32_t pc = r + 16 * j;
-        if (16 * j >= P) break;  // uniform: rows of D <= 128 need one round
-        u32x4 w = vw[j];
-        if (vfresh && pc < P) w = *reinterpret_cast<const u32x4 *>(&vnew[8 * pc]);
-        const uint32_t W[4] = {w.x, w.y, w.z, w.w};
-        float acc[8 * GP];
-#pragma unroll
-        for (int g = 0; g < GP; ++g) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                acc[8 * g + 2 * e] = pr[g] * __uint_as_float(W[e] << 16);
-                acc[8 * g + 2 * e + 1] = pr[g] * __uint_as_float(W[e] & 0xFFFF0000u);
-            }
+        for (uint32_t p = 0; p < kSplitLen; ++p) {
+            const float w = sc[g][p];
+            const uint2 vv = *reinterpret_cast<const uint2 *>(&vt[p * D + d]);
+            a0 = fmaf(w, __uint_as_float(vv.x << 16), a0);
+            a1 = fmaf(w, __uint_as_float(vv.x & 0xFFFF0000u), a1);
+            a2 = fmaf(w, __uint_as_float(vv.y << 16), a2);
+            a3 = fmaf(w, __uint_as_float(vv.y & 0xFFFF0000u), a3);
         }
-        row16_reduce<8 * GP>(acc, c);
-        // lane c holds values (GP / 2) c .. : index i = 8 g + e
-        constexpr int kPer = 8 * GP >= 16 ? 8 * GP / 16 : 1;
-        if (pc < P) {
-#pragma unroll
-            for (int t = 0; t < kPer; ++t) {
-                const uint32_t i = (8 * GP >= 16) ? c * kPer + t : c / (16 / (8 * GP));
-                const uint32_t g = i / 8, e = i % 8;
-                const bool writer = 8 * GP >= 16 || (c % (16 / (8 * GP))) == 0;
-                if (writer && g < G) out[2 * G + g * D + 8 * pc + e] = acc[t];
-            }
-        }
+        float *o = out + 2 * G + g * D + d;  // 8-byte aligned (G (D + 2) may be odd * 2)
+        reinterpret_cast<float2 *>(o)[0] = make_float2(a0, a1);
+        reinterpret_cast<float2 *>(o)[1] = make_float2(a2, a3);
     }
     // deferred global stores
     if (r < G && c == 0) {

@@ -124,7 +124,9 @@ def test_rope_append_and_attention(kq):
 
 
 @pytest.mark.parametrize("B,H,KVH,D,ctx,pos", [(3, 8, 2, 64, 12, [5, 11, 0]), (2, 16, 2, 128, 513, [512, 130]),
-                                               (1, 4, 4, 32, 200, [199]), (2, 32, 2, 128, 70, [64, 70])])
+                                               (1, 4, 4, 32, 200, [199]), (2, 32, 2, 128, 70, [64, 70]),
+                                               (2, 8, 4, 256, 40, [39, 17]), (1, 12, 4, 96, 33, [32]),
+                                               (2, 6, 1, 8, 20, [3, 19])])
 def test_rope_attention_matches_two_step_path(kq, B, H, KVH, D, ctx, pos):
     """Split-context attention with fused RoPE/append against kr_rope_kv_append + kr_attention_decode
     on the same inputs: identical caches, outputs within a few bf16 ulps (f32 summation order differs).
