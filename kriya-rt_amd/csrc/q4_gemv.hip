@@ -352,21 +352,35 @@ __global__ __launch_bounds__(256) void q4_moe_gemv_kernel(MoeGemvArgs a) {
     const bool live = (uint32_t)lane < nchunks;
     const uint32_t c = live ? (uint32_t)lane : 0u;
 
+    // A fixed, unrolled sequence with uniform guards and clamped loads, not a loop: the compiler
+    // waits for every load in flight before entering a loop, which would serialise this lookup
+    // behind sorted[p].
     auto expert_of = [&](uint32_t p) -> uint32_t {
         uint32_t e = 0;
-        for (uint32_t j0 = 0; j0 < a.experts; j0 += kWave) {
-            const uint32_t j = j0 + (uint32_t)lane;
-            const bool le = j < a.experts && a.offsets[j + 1] <= p;
-            e += (uint32_t)__popcll(__ballot(le));
+#pragma unroll
+        for (uint32_t i = 0; i < kMaxExperts / kWave; ++i) {
+            if (i * kWave < a.experts) {
+                const uint32_t j = i * kWave + (uint32_t)lane;
+                const uint32_t end = a.offsets[min(j, a.experts - 1) + 1];
+                e += (uint32_t)__popcll(__ballot(j < a.experts && end <= p));
+            }
         }
         return e;
     };
-    // per-position state: views of the expert's matrices, the x pairs, the output row base
+    // per-position state: views of the expert's matrices, the x pairs, the output row base.
+    // Only the views depend on the expert; a position change requests sorted[p] with the
+    // expert lookup, then the tile's words, then the x words, and the x pairs are built just
+    // before the next dot: the chain to the first words is one round trip, not three.
     Q4Mat A = a.w, B = a.w2;
     GemvOut o{nullptr, nullptr, a.act, 0};
     XChunk xc;
-    uint32_t cur_p = 0xFFFFFFFFu;
+    uint32_t X[16];
+    uint32_t cur_p = 0xFFFFFFFFu, cur_xr = 0;
     auto enter = [&](uint32_t p) {
+        // sorted[p] through a lane-varying zero: a uniform load is moved to a scalar register
+        // right away (a wait before the expert lookup is even requested); this one stays in a
+        // vector register until its use
+        const uint32_t sp = a.sorted[p + __builtin_amdgcn_mbcnt_lo(0u, 0u)];
         const uint32_t e = expert_of(p);
         const size_t r0 = (size_t)e * a.rows;
         A.qw = a.w.qw + r0 * wpr;
@@ -376,14 +390,13 @@ __global__ __launch_bounds__(256) void q4_moe_gemv_kernel(MoeGemvArgs a) {
         B.sc = a.w2.sc + r0 * groups;
         B.bi = a.w2.bi + r0 * groups;
         A.n = B.n = a.rows;
-        const uint32_t sp = a.sorted[p];
-        const uint32_t xr = a.x_div ? sp / a.x_div : p;
+        cur_xr = a.x_div ? sp / a.x_div : p;
         const uint32_t orow = a.out_scatter ? sp : p;
         const size_t esz = (EPI == kStoreF32 || EPI == kAccF32 || EPI == kGateUpF32) ? 4 : 2;
         o.out = reinterpret_cast<char *>(a.out) + (size_t)orow * a.ldo * esz;
-        load_xchunk(xc, a.x + (size_t)xr * K, c, kSelLo, kSelHi);
         cur_p = p;
     };
+    auto load_x = [&] { load_xwords(X, a.x + (size_t)cur_xr * K, c); };
 
     const u32x4 *rq[R];
     const uint16_t *rs[R];
@@ -402,7 +415,11 @@ __global__ __launch_bounds__(256) void q4_moe_gemv_kernel(MoeGemvArgs a) {
     uint32_t t = t_begin;
     enter(t / a.tiles_per);
     fetch(t % a.tiles_per);
+    load_x();
+    bool x_new = true;
     for (;;) {
+        if (x_new) build_xchunk(xc, X, kSelLo, kSelHi);
+        x_new = false;
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -414,8 +431,14 @@ __global__ __launch_bounds__(256) void q4_moe_gemv_kernel(MoeGemvArgs a) {
         const uint32_t tn = t + 1;
         if (tn < t_end) {
             const uint32_t pn = tn / a.tiles_per;
-            if (pn != cur_p) enter(pn);
-            fetch(tn % a.tiles_per);
+            if (pn != cur_p) {
+                enter(pn);
+                fetch(tn % a.tiles_per);
+                load_x();
+                x_new = true;
+            } else {
+                fetch(tn % a.tiles_per);
+            }
         }
         const float tot = wave_reduce_rows<R>(acc, lane);
         tile_epilogue<R, EPI>(tot, lane, lt, a.rows, oc, 0.0f);
