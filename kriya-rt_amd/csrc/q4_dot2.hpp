@@ -259,7 +259,7 @@ __device__ __forceinline__ GemvProblem pick_problem(const GemvBatch &gb, int pi,
 // needs) are requested before the current tile is reduced and stored.
 // M > 1: x holds M token rows of k elements; every unpacked word is
 // multiplied with all of them (no RMSNorm, single problem).
-template <int R, int C, int EPI, bool kMulti, int M = 1>
+template <int R, int C, int EPI, bool kMulti, int M = 1, bool kNorm = false>
 __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16_t *__restrict__ x, uint32_t t0,
                                                uint32_t nwaves) {
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
@@ -341,13 +341,21 @@ __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16
 #pragma unroll
         for (int i = 0; i < C; ++i)
             if (live[i]) load_xwords(X[i], x, lane + kWave * i);
-        if (gb.ln_w) {
+        if constexpr (kNorm) {
+            // x is RMS-normalised before its pairs are built (bf16(x * rsqrt(mean(x^2) + eps) * w),
+            // kr_rmsnorm's arithmetic).  The first tile's words are requested before the norm's
+            // arithmetic: it waits for x and ln_w only (issued first), while the words stay in
+            // flight.
             uint32_t Wl[C][16];
+#pragma unroll
+            for (int i = 0; i < C; ++i)
+                if (live[i]) load_xwords(Wl[i], gb.ln_w, lane + kWave * i);
+            pre = fetch(t);
+            __builtin_amdgcn_sched_barrier(0);  // the norm's arithmetic stays after the requests
             float ss = 0.0f;
 #pragma unroll
             for (int i = 0; i < C; ++i) {
                 if (live[i]) {
-                    load_xwords(Wl[i], gb.ln_w, lane + kWave * i);
 #pragma unroll
                     for (int e = 0; e < 16; ++e) {
                         const float a = __uint_as_float(X[i][e] << 16), b = __uint_as_float(X[i][e] & 0xFFFF0000u);
@@ -370,11 +378,15 @@ __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16
                     }
                 }
             }
-        }
 #pragma unroll
-        for (int i = 0; i < C; ++i)
-            if (live[i]) build_xchunk(xc[i][0], X[i], kSelLo, kSelHi);
-        pre = fetch(t);
+            for (int i = 0; i < C; ++i)
+                if (live[i]) build_xchunk(xc[i][0], X[i], kSelLo, kSelHi);
+        } else {
+#pragma unroll
+            for (int i = 0; i < C; ++i)
+                if (live[i]) build_xchunk(xc[i][0], X[i], kSelLo, kSelHi);
+            pre = fetch(t);
+        }
     }
 
     for (;;) {

@@ -39,10 +39,10 @@ namespace kr {
 
 // kMulti: the batch may hold several problems (np > 1); single-problem
 // launches skip the per-tile problem selection.
-template <int R, int C, int EPI, bool kMulti>
+template <int R, int C, int EPI, bool kMulti, bool kNorm = false>
 __global__ __launch_bounds__(256) void q4_gemv_wave_kernel(GemvBatch gb, const uint16_t *__restrict__ x) {
-    gemv_wave_loop<R, C, EPI, kMulti>(gb, x, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave),
-                              gridDim.x * 4);
+    gemv_wave_loop<R, C, EPI, kMulti, 1, kNorm>(gb, x, blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave),
+                                              gridDim.x * 4);
 }
 
 // The wave kernel for M = 2..4 tokens (x holds M rows), two rows per tile,
@@ -232,19 +232,35 @@ static hipError_t launch_wave_batch(GemvBatch &gb, const uint16_t *x, hipStream_
     gb.tiles = tiles;
     const uint32_t blocks = cap_blocks((tiles + 3) / 4, (uint32_t)tuning().gemv_persistent_blocks);
     const bool c1 = gb.p[0].A.k <= 64 * 32;
+    // the norm-fused kernels (x RMS-normalised in the kernel) exist for the epilogues the fused
+    // norms use: gate/up (kr_rmsnorm_q4_mlp) and the stores (kr_rmsnorm_q4_qkv)
+    constexpr bool kNormable = EPI == kGateUpBF16 || EPI == kStoreF32 || EPI == kStoreBF16;
+    if (gb.ln_w && !kNormable) return hipErrorInvalidValue;
+#define KR_WAVE(CC, MULTI)                                                                                       \
+    do {                                                                                                         \
+        if constexpr (kNormable) {                                                                               \
+            if (gb.ln_w) {                                                                                       \
+                hipLaunchKernelGGL((q4_gemv_wave_kernel<R, CC, EPI, MULTI, true>), dim3(blocks), dim3(256), 0, s, \
+                                   gb, x);                                                                       \
+                break;                                                                                           \
+            }                                                                                                    \
+        }                                                                                                        \
+        hipLaunchKernelGGL((q4_gemv_wave_kernel<R, CC, EPI, MULTI, false>), dim3(blocks), dim3(256), 0, s, gb, x); \
+    } while (0)
     if (gb.np == 1) {
         if (c1)
-            hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 1, EPI, false>), dim3(blocks), dim3(256), 0, s, gb, x);
+            KR_WAVE(1, false);
         else
-            hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 2, EPI, false>), dim3(blocks), dim3(256), 0, s, gb, x);
+            KR_WAVE(2, false);
     } else if constexpr (EPI == kStoreF32 || EPI == kStoreBF16) {
         if (c1)
-            hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 1, EPI, true>), dim3(blocks), dim3(256), 0, s, gb, x);
+            KR_WAVE(1, true);
         else
-            hipLaunchKernelGGL((q4_gemv_wave_kernel<R, 2, EPI, true>), dim3(blocks), dim3(256), 0, s, gb, x);
+            KR_WAVE(2, true);
     } else {
         return hipErrorInvalidValue;  // batches of several problems use the store epilogues only
     }
+#undef KR_WAVE
     return hipGetLastError();
 }
 
