@@ -499,7 +499,9 @@ static hipError_t launch_tokens_m(const Q4Mat &a, const Q4Mat &b, const uint16_t
     if constexpr (!kGateUp) {
         if (chunks <= 512) {
             const uint32_t blocks = (a.n + 7) / 8;
-            hipLaunchKernelGGL((q4_gemv_rows_kernel<8, EPI, M>), dim3(blocks), dim3(1024), 0, s, a, x, o);
+            // one row group of 512 threads: each thread's x words serve all 8 rows of the block
+            // (x is M times the weight bytes per chunk here; measured 3-4 % faster than two groups)
+            hipLaunchKernelGGL((q4_gemv_rows_kernel<8, EPI, M, 1>), dim3(blocks), dim3(512), 0, s, a, x, o);
             return hipGetLastError();
         }
     }
