@@ -238,21 +238,23 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(
 // block owns 16 positions of one sequence and one kv head and all G <= GP
 // query heads that share it (GQA: each key and value row is read once for the
 // G heads).  Thread t is lane c = t % 16 of row r = t / 16.  It
-//   0. requests, before anything else, its key piece (position r, dims 8c..)
-//      and its value piece (position c, dims 8r..) -- the rows of D > 128 in a
-//      second piece each;
+//   0. requests, before anything else, its key piece in the matrix-core layout
+//      (position t % 16, dims 32 (t / 64) + 8 ((t / 16) % 4)) and its value
+//      piece (position c, dims 8r..) -- the rows of D > 128 in a second piece
+//      each;
 //   1. rotates the G query heads (bf16-rounded, as kr_rope_kv_append stores
 //      them) into LDS;
 //   2. if the block holds the new position, rotates k and writes k and v into
-//      the cache (kr_rope_kv_append's arithmetic); its own dots take that row
-//      from LDS;
-//   3. scores: the 16 lanes of a row split the key row; their G partial dots
-//      are summed by a transposing butterfly (lane c ends with head c);
-//   4. per head (a row of 16 lanes, one per position): the slice's max m and
-//      sum l of exp(score - m);
-//   5. values: lane c of row r multiplies its value piece by the G
-//      probabilities of position c; the transposing butterfly over the row
-//      leaves lane c with 8 GP / 16 consecutive (head, dim) sums.
+//      the cache (kr_rope_kv_append's arithmetic); its own scores take that
+//      row from LDS;
+//   3. scores: wave w multiplies the 32-dim steps w [and w + 4] of q (head
+//      rows) with the key slice on the matrix cores (v_mfma_f32_16x16x32_bf16;
+//      bf16 products are exact, sums f32); the value tile goes to LDS over q;
+//   4. per head (a row of 16 lanes, one per position): the four waves' partial
+//      scores added in wave order, the slice's max m and sum l of
+//      exp(score - m);
+//   5. values: thread (head, 4 dims) sums its 16 positions in order from the
+//      LDS value tile.
 // The partial (m, l, acc) of each (sequence, kv head, slice) goes to the
 // workspace; attention_combine_kernel merges the slices in slice order:
 //   out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,  M = max_s m_s
@@ -260,28 +262,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(
 constexpr uint32_t kSplitLen = 16;   // positions per slice
 
 __device__ __forceinline__ float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
-
-// Sum of R values over the 16 lanes of a row, halving the value set per step:
-// lane c ends with the totals of values (R/16) c .. (R/16) c + R/16 - 1
-// (R >= 16), or of value c / (16/R) (R < 16).  Fixed order.
-template <int R>
-__device__ __forceinline__ void row16_reduce(float (&v)[R], uint32_t c) {
-    int mask = 8;
-#pragma unroll
-    for (int half = R / 2; half >= 1 && mask >= 1; half >>= 1, mask >>= 1) {
-        const bool upper = (c & (uint32_t)mask) != 0;
-#pragma unroll
-        for (int i = 0; i < half; ++i) {
-            const float send = upper ? v[i] : v[i + half];
-            const float keep = upper ? v[i + half] : v[i];
-            v[i] = keep + __shfl_xor(send, mask);
-        }
-    }
-    if constexpr (R < 16) {
-#pragma unroll
-        for (int m = 8 / R; m >= 1; m >>= 1) v[0] += __shfl_xor(v[0], m);
-    }
-}
 
 template <int GP>
 __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q, const uint16_t *k, const uint16_t *v,
@@ -294,7 +274,8 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
                                        ? GP * kGlueMaxHeadDim
                                        : kSplitLen * kGlueMaxHeadDim / 2;
     __shared__ __align__(16) float qs[kQsFloats];
-    __shared__ float sc[GP][kSplitLen];                        // scores, then exp(score - m)
+    __shared__ float sc[GP][kSplitLen];                        // exp(score - m)
+    __shared__ float sp[4][16][kSplitLen];                     // per-wave partial scores [wave][head][pos]
     __shared__ __align__(16) float knew[kGlueMaxHeadDim];
     __shared__ __align__(16) uint16_t vnew[kGlueMaxHeadDim];
     const uint32_t tid = threadIdx.x, r = tid >> 4, c = tid & 15;
@@ -314,13 +295,16 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
     // Loads are unconditional, from clamped (in-bounds) addresses; what they should not
     // contribute is zeroed where it is used.  A conditional load merged with a default value
     // makes the compiler wait for every load in flight at the merge.
-    const uint32_t kr_ = p0 + r < max_ctx ? r : 0u, vc_ = p0 + c < max_ctx ? c : 0u;
+    // key pieces in the matrix-core layout of the scores: thread (wave w, lane l) takes position
+    // p0 + (l & 15) and piece 4 w + (l >> 4) [+16], i.e. dims 32 w + 8 (l >> 4) [+128]
+    const uint32_t kp = tid & 15, kc = 4 * (tid >> 6) + ((tid >> 4) & 3);
+    const uint32_t kr_ = p0 + kp < max_ctx ? kp : 0u, vc_ = p0 + c < max_ctx ? c : 0u;
     u32x4 kw[2], vw[2];
-    kw[0] = *reinterpret_cast<const u32x4 *>(kbase + kr_ * row_stride + 8 * min(c, P - 1));
+    kw[0] = *reinterpret_cast<const u32x4 *>(kbase + kr_ * row_stride + 8 * min(kc, P - 1));
     vw[0] = *reinterpret_cast<const u32x4 *>(vbase + vc_ * row_stride + 8 * min(r, P - 1));
     kw[1] = vw[1] = u32x4{0, 0, 0, 0};
     if (P > 16) {  // rows of D > 128: a second piece (uniform)
-        kw[1] = *reinterpret_cast<const u32x4 *>(kbase + kr_ * row_stride + 8 * min(c + 16, P - 1));
+        kw[1] = *reinterpret_cast<const u32x4 *>(kbase + kr_ * row_stride + 8 * min(kc + 16, P - 1));
         vw[1] = *reinterpret_cast<const u32x4 *>(vbase + vc_ * row_stride + 8 * min(r + 16, P - 1));
     }
     constexpr uint32_t kQPairs = GP * kGlueMaxHeadDim / 2 / 256;  // query pairs per thread: G * D/2 <= 256 max(kQPairs, 1)
@@ -397,48 +381,49 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
         kn1 = k1;  // block's outstanding global stores
     }
     __syncthreads();
-    // 3. scores of position p0 + r: lanes split the key row, then the transposing butterfly
+    // 3. scores on the matrix cores: wave w multiplies the 32-dim steps w and w + 4 (D > 128) of
+    //    q (16 head rows, bf16 values) with the key slice (dims x 16 positions), one
+    //    v_mfma_f32_16x16x32_bf16 per step; the products are exact and sum in f32.  The four
+    //    waves' partial tiles are added in wave order in step 4.
     {
-        float dot[GP];
-#pragma unroll
-        for (int g = 0; g < GP; ++g) dot[g] = 0.0f;
-        const bool fresh = has_new && p0 + r == pos;
+        const uint32_t wv = tid >> 6, l = tid & 63, row = l & 15, kq = l >> 4;
+        const bool fresh = has_new && p0 + kp == pos;
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (uint32_t j = 0; j < 2; ++j) {
-            const uint32_t pc = c + 16 * j;
-            if (pc < P && p0 + r < p1) {
-                float kf[8] = {__uint_as_float(kw[j].x << 16), __uint_as_float(kw[j].x & 0xFFFF0000u),
-                               __uint_as_float(kw[j].y << 16), __uint_as_float(kw[j].y & 0xFFFF0000u),
-                               __uint_as_float(kw[j].z << 16), __uint_as_float(kw[j].z & 0xFFFF0000u),
-                               __uint_as_float(kw[j].w << 16), __uint_as_float(kw[j].w & 0xFFFF0000u)};
-                if (fresh) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) kf[e] = knew[8 * pc + e];
+            const uint32_t step = wv + 4 * j, d0 = 32 * step + 8 * kq;
+            if (32 * step >= D) break;  // uniform
+            uint32_t av[4] = {0, 0, 0, 0}, bv[4] = {0, 0, 0, 0};
+            if (d0 < D) {
+                if (row < G) {  // q values are bf16-rounded: their bf16 bits are exact
+                    const f32x4 qa = *reinterpret_cast<const f32x4 *>(&qs[row * D + d0]);
+                    const f32x4 qb = *reinterpret_cast<const f32x4 *>(&qs[row * D + d0 + 4]);
+                    av[0] = (__float_as_uint(qa.x) >> 16) | (__float_as_uint(qa.y) & 0xFFFF0000u);
+                    av[1] = (__float_as_uint(qa.z) >> 16) | (__float_as_uint(qa.w) & 0xFFFF0000u);
+                    av[2] = (__float_as_uint(qb.x) >> 16) | (__float_as_uint(qb.y) & 0xFFFF0000u);
+                    av[3] = (__float_as_uint(qb.z) >> 16) | (__float_as_uint(qb.w) & 0xFFFF0000u);
                 }
-#pragma unroll
-                for (int g = 0; g < GP; ++g) {
-                    if ((uint32_t)g < G) {
-                        const f32x4 qa = *reinterpret_cast<const f32x4 *>(&qs[g * D + 8 * pc]);
-                        const f32x4 qb = *reinterpret_cast<const f32x4 *>(&qs[g * D + 8 * pc + 4]);
-                        float d0 = dot[g];
-                        d0 = fmaf(qa.x, kf[0], d0);
-                        d0 = fmaf(qa.y, kf[1], d0);
-                        d0 = fmaf(qa.z, kf[2], d0);
-                        d0 = fmaf(qa.w, kf[3], d0);
-                        d0 = fmaf(qb.x, kf[4], d0);
-                        d0 = fmaf(qb.y, kf[5], d0);
-                        d0 = fmaf(qb.z, kf[6], d0);
-                        d0 = fmaf(qb.w, kf[7], d0);
-                        dot[g] = d0;
-                    }
+                if (fresh) {  // the new (rotated) key, bf16-rounded in knew
+                    const f32x4 ka = *reinterpret_cast<const f32x4 *>(&knew[d0]);
+                    const f32x4 kb = *reinterpret_cast<const f32x4 *>(&knew[d0 + 4]);
+                    bv[0] = (__float_as_uint(ka.x) >> 16) | (__float_as_uint(ka.y) & 0xFFFF0000u);
+                    bv[1] = (__float_as_uint(ka.z) >> 16) | (__float_as_uint(ka.w) & 0xFFFF0000u);
+                    bv[2] = (__float_as_uint(kb.x) >> 16) | (__float_as_uint(kb.y) & 0xFFFF0000u);
+                    bv[3] = (__float_as_uint(kb.z) >> 16) | (__float_as_uint(kb.w) & 0xFFFF0000u);
+                } else {
+                    bv[0] = kw[j].x;
+                    bv[1] = kw[j].y;
+                    bv[2] = kw[j].z;
+                    bv[3] = kw[j].w;
                 }
             }
+            const u32x4 a4 = {av[0], av[1], av[2], av[3]}, b4 = {bv[0], bv[1], bv[2], bv[3]};
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a4),
+                                                          __builtin_bit_cast(bf16x8_t, b4), acc, 0, 0, 0);
         }
-        row16_reduce<GP>(dot, c);
-        // lane c holds head c (GP >= 16) or head c / (16 / GP) (GP < 16, every such lane holds it)
-        const uint32_t g = GP >= 16 ? c : c / (16 / GP);
-        const bool writer = GP >= 16 || (c % (16 / GP)) == 0;
-        if (writer && g < G) sc[g][r] = p0 + r < p1 ? dot[0] * (1.0f / sqrtf((float)D)) : -INFINITY;
+        // lane l holds rows (heads) 4 (l >> 4) + e of column (position) l & 15
+#pragma unroll
+        for (uint32_t e = 0; e < 4; ++e) sp[wv][4 * kq + e][row] = acc[e];
     }
     __syncthreads();
     // 4a. the value tile into LDS, over q's rows (read only by the scores, done): row c =
@@ -461,7 +446,8 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
     // 4b. per head: row r takes head r, lane c position p0 + c
     float m_keep = 0.0f, l_keep = 0.0f;
     if (r < G) {
-        const float x = sc[r][c];
+        const float dot = ((sp[0][r][c] + sp[1][r][c]) + sp[2][r][c]) + sp[3][r][c];
+        const float x = p0 + c < p1 ? dot * (1.0f / sqrtf((float)D)) : -INFINITY;
         float m = x;
 #pragma unroll
         for (int sh = 8; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
