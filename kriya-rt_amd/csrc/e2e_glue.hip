@@ -253,8 +253,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(
 //   4. per head (a row of 16 lanes, one per position): the four waves' partial
 //      scores added in wave order, the slice's max m and sum l of
 //      exp(score - m);
-//   5. values: thread (head, 4 dims) sums its 16 positions in order from the
-//      LDS value tile.
+//   5. values: wave w multiplies the probabilities (bf16 hi + lo) with the
+//      16-dim tiles w, w + 4, ... of the LDS value tile on the matrix cores.
 // The partial (m, l, acc) of each (sequence, kv head, slice) goes to the
 // workspace; attention_combine_kernel merges the slices in slice order:
 //   out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s,  M = max_s m_s
@@ -460,25 +460,37 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
         l_keep = l;
     }
     __syncthreads();
-    // 5. values: thread (head g, dims 4 d4 .. + 3) sums its 16 positions in order from the LDS
-    //    tile -- no cross-lane reduction (positions past the sequence have weight 0 and zero
-    //    values)
-    const uint32_t D4 = D / 4;
-    for (uint32_t it = tid; it < G * D4; it += 256) {
-        const uint32_t g = it / D4, d = 4 * (it % D4);
-        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    // 5. values on the matrix cores, per 16-dim tile (wave w takes tiles w, w + 4, ...):
+    //    out[head][dim] = sum_p P[head][p] V[p][dim] with v_mfma_f32_16x16x16_bf16.  V is bf16 in
+    //    the LDS tile; P (f32) is split into bf16 hi + lo (P = hi + lo to 2^-17), two products that
+    //    are exact and sum in f32.  Positions past the sequence have P = 0 and zero values.
+    {
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        const uint32_t wv = tid >> 6, l = tid & 63, row = l & 15, kq = l >> 4;
+        s16x4 ahi, alo;  // A: P[head row][positions 4 kq .. + 3]
 #pragma unroll
-        for (uint32_t p = 0; p < kSplitLen; ++p) {
-            const float w = sc[g][p];
-            const uint2 vv = *reinterpret_cast<const uint2 *>(&vt[p * D + d]);
-            a0 = fmaf(w, __uint_as_float(vv.x << 16), a0);
-            a1 = fmaf(w, __uint_as_float(vv.x & 0xFFFF0000u), a1);
-            a2 = fmaf(w, __uint_as_float(vv.y << 16), a2);
-            a3 = fmaf(w, __uint_as_float(vv.y & 0xFFFF0000u), a3);
+        for (uint32_t i = 0; i < 4; ++i) {
+            const float pv = row < G ? sc[row][4 * kq + i] : 0.0f;
+            const uint32_t hi = f32_to_bf16(pv);
+            ahi[i] = (short)hi;
+            alo[i] = (short)f32_to_bf16(pv - bf16_to_f32(hi));
         }
-        float *o = out + 2 * G + g * D + d;  // 8-byte aligned (G (D + 2) may be odd * 2)
-        reinterpret_cast<float2 *>(o)[0] = make_float2(a0, a1);
-        reinterpret_cast<float2 *>(o)[1] = make_float2(a2, a3);
+        const uint32_t ntile = (D + 15) / 16;
+        for (uint32_t t = wv; t < ntile; t += 4) {
+            const uint32_t d = 16 * t + row;  // B: V[positions 4 kq .. + 3][dim d]
+            s16x4 bv;
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) bv[i] = d < D ? (short)vt[(4 * kq + i) * D + d] : (short)0;
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ahi, bv, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(alo, bv, acc, 0, 0, 0);
+            // lane l holds heads 4 kq + e of dim d
+#pragma unroll
+            for (uint32_t e = 0; e < 4; ++e) {
+                const uint32_t h = 4 * kq + e;
+                if (h < G && d < D) out[2 * G + h * D + d] = acc[e];
+            }
+        }
     }
     // deferred global stores
     if (r < G && c == 0) {
