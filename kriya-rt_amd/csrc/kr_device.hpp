@@ -37,6 +37,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float v) {
     return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
 }
 
+// Two values rounded to bf16 by v_cvt_pk_bf16_f32 (round to nearest even): for every input but
+// NaN (whose payload it may change) the bits of f32_to_bf16 above, in one instruction.
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t h = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, h);
+}
+
 // ---- nibble unpack without conversion instructions.
 // For j in 0..3, bits 4j..4j+3 and 16+4j..16+4j+3 of w (elements j and j+4 of
 // the word) are placed under the bf16 pattern 0x4300 (= 128.0, ulp 1), giving

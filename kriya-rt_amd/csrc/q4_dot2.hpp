@@ -374,7 +374,7 @@ __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16
                         const float lo = __uint_as_float(X[i][e] << 16) * scale * __uint_as_float(Wl[i][e] << 16);
                         const float hi =
                             __uint_as_float(X[i][e] & 0xFFFF0000u) * scale * __uint_as_float(Wl[i][e] & 0xFFFF0000u);
-                        X[i][e] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+                        X[i][e] = pack_bf16_rne(lo, hi);
                     }
                 }
             }

@@ -344,7 +344,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             for (int i = 0; i < 4; ++i) {
                 const float lo = __uint_as_float(X[i] << 16) * scale * __uint_as_float(W[i] << 16);
                 const float hi = __uint_as_float(X[i] & 0xFFFF0000u) * scale * __uint_as_float(W[i] & 0xFFFF0000u);
-                X[i] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+                X[i] = pack_bf16_rne(lo, hi);
             }
             raw[st] = u32x4{X[0], X[1], X[2], X[3]};
         }
