@@ -273,7 +273,9 @@ __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16
     const uint32_t kMagic = vgpr_const(0x43004300u);
     const uint32_t kSelLo = sgpr_const(0x05040100u);
     const uint32_t kSelHi = sgpr_const(0x07060302u);
-    if (t >= tiles) return;
+    // (the norm-fused kernel returns after its block-wide prologue: every wave of the block
+    // reaches that prologue's barriers)
+    if (!kNorm && t >= tiles) return;
 
     // lane's chunks (c < nchunks is lane-dependent only through c = lane + 64 i)
     bool live[C];
@@ -338,50 +340,82 @@ __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16
         }
     } else {
         uint32_t X[C][16];
-#pragma unroll
-        for (int i = 0; i < C; ++i)
-            if (live[i]) load_xwords(X[i], x, lane + kWave * i);
         if constexpr (kNorm) {
-            // x is RMS-normalised before its pairs are built (bf16(x * rsqrt(mean(x^2) + eps) * w),
-            // kr_rmsnorm's arithmetic).  The first tile's words are requested before the norm's
-            // arithmetic: it waits for x and ln_w only (issued first), while the words stay in
-            // flight.
-            uint32_t Wl[C][16];
+            // The block RMS-normalises x once, into LDS (bf16(x * rsqrt(mean(x^2) + eps) * w),
+            // kr_rmsnorm's arithmetic): thread t loads 16-byte units t and t + 256 of x and ln_w,
+            // the four waves' sums of squares meet in LDS (added in wave order), each thread
+            // scales its units, and every lane reads its chunks back.  Per-wave norms read x and
+            // ln_w once per wave and repeated the arithmetic.  The first tile's words are
+            // requested before the norm waits for x.  Every wave runs this prologue (its loads
+            // depend only on the thread and K; a wave without a tile requests a valid tile it
+            // never uses) and so reaches both barriers; such a wave returns after them.
+            static_assert(C <= 2, "k <= 4096: at most two 16-byte units per thread");
+            __shared__ u32x4 s_xn[2 * 256];
+            __shared__ float s_ss[4];
+            const uint32_t tid = threadIdx.x, units = K >> 3;
+            u32x4 xu[2], wu[2];
 #pragma unroll
-            for (int i = 0; i < C; ++i)
-                if (live[i]) load_xwords(Wl[i], gb.ln_w, lane + kWave * i);
-            pre = fetch(t);
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t uu = min(tid + 256u * j, units - 1);
+                xu[j] = *reinterpret_cast<const u32x4 *>(x + 8 * (size_t)uu);
+                wu[j] = *reinterpret_cast<const u32x4 *>(gb.ln_w + 8 * (size_t)uu);
+            }
+            pre = fetch(t < tiles ? t : tiles - 1);
             __builtin_amdgcn_sched_barrier(0);  // the norm's arithmetic stays after the requests
             float ss = 0.0f;
 #pragma unroll
-            for (int i = 0; i < C; ++i) {
-                if (live[i]) {
+            for (int j = 0; j < 2; ++j) {
+                if (tid + 256u * j < units) {
+                    const uint32_t W4[4] = {xu[j].x, xu[j].y, xu[j].z, xu[j].w};
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const float a = __uint_as_float(X[i][e] << 16), b = __uint_as_float(X[i][e] & 0xFFFF0000u);
+                    for (int e = 0; e < 4; ++e) {
+                        const float a = __uint_as_float(W4[e] << 16), b = __uint_as_float(W4[e] & 0xFFFF0000u);
                         ss = fmaf(a, a, ss);
                         ss = fmaf(b, b, ss);
                     }
                 }
             }
             ss = wave_sum(ss);
-            const float scale = 1.0f / sqrtf(ss / (float)K + gb.eps);
+            if (lane == 0) s_ss[tid >> 6] = ss;
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // LDS only: the words stay in flight
+            const float scale = 1.0f / sqrtf((((s_ss[0] + s_ss[1]) + s_ss[2]) + s_ss[3]) / (float)K + gb.eps);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (tid + 256u * j < units) {
+                    const uint32_t X4[4] = {xu[j].x, xu[j].y, xu[j].z, xu[j].w};
+                    const uint32_t L4[4] = {wu[j].x, wu[j].y, wu[j].z, wu[j].w};
+                    uint32_t o[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float lo = __uint_as_float(X4[e] << 16) * scale * __uint_as_float(L4[e] << 16);
+                        const float hi =
+                            __uint_as_float(X4[e] & 0xFFFF0000u) * scale * __uint_as_float(L4[e] & 0xFFFF0000u);
+                        o[e] = pack_bf16_rne(lo, hi);
+                    }
+                    s_xn[tid + 256u * j] = u32x4{o[0], o[1], o[2], o[3]};
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (t >= tiles) return;
 #pragma unroll
             for (int i = 0; i < C; ++i) {
                 if (live[i]) {
+                    const uint32_t c = lane + kWave * i;
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const float lo = __uint_as_float(X[i][e] << 16) * scale * __uint_as_float(Wl[i][e] << 16);
-                        const float hi =
-                            __uint_as_float(X[i][e] & 0xFFFF0000u) * scale * __uint_as_float(Wl[i][e] & 0xFFFF0000u);
-                        X[i][e] = pack_bf16_rne(lo, hi);
+                    for (int q = 0; q < 4; ++q) {
+                        const u32x4 v = s_xn[4 * c + q];
+                        X[i][4 * q] = v.x;
+                        X[i][4 * q + 1] = v.y;
+                        X[i][4 * q + 2] = v.z;
+                        X[i][4 * q + 3] = v.w;
                     }
+                    build_xchunk(xc[i][0], X[i], kSelLo, kSelHi);
                 }
             }
+        } else {
 #pragma unroll
             for (int i = 0; i < C; ++i)
-                if (live[i]) build_xchunk(xc[i][0], X[i], kSelLo, kSelHi);
-        } else {
+                if (live[i]) load_xwords(X[i], x, lane + kWave * i);
 #pragma unroll
             for (int i = 0; i < C; ++i)
                 if (live[i]) build_xchunk(xc[i][0], X[i], kSelLo, kSelHi);

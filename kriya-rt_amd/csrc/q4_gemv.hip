@@ -230,6 +230,7 @@ static hipError_t launch_wave_batch(GemvBatch &gb, const uint16_t *x, hipStream_
         tiles += tiles_for<EPI>(gb.p[i].A.n, R);
     }
     gb.tiles = tiles;
+    if (tiles == 0) return hipSuccess;  // (the norm-fused kernel requests tile min(t, tiles - 1))
     const uint32_t blocks = cap_blocks((tiles + 3) / 4, (uint32_t)tuning().gemv_persistent_blocks);
     const bool c1 = gb.p[0].A.k <= 64 * 32;
     // the norm-fused kernels (x RMS-normalised in the kernel) exist for the epilogues the fused
