@@ -95,6 +95,10 @@ const char *kr_last_error(void);
 #define KR_OPT_SPLITK_TICKETS 12        /* kr_q4_mlp at 2 <= m <= 16: 1 (default) the down projection's
                                            K split is reduced by the last block of each run (one launch),
                                            0 by a second launch */
+#define KR_OPT_ATTN_MERGE_WAVE 13       /* kr_rope_attention_decode: 1 (default) the slices of a head are merged
+                                           by a kernel without block barriers when there are <= 64 of
+                                           them and D is a power of two from 8 to 256, 0 always by the
+                                           general kernel (same bits) */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 

@@ -584,6 +584,52 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float *par
     if (tid < D) out[((size_t)b * q_heads + h) * D + tid] = (uint16_t)f32_to_bf16(acc / L);
 }
 
+// grid (q_heads, batch), 256 threads: the merge of at most 64 slices for D = 4 DW with DW | 64.
+// Wave w takes dims [w DW, (w + 1) DW) of head h; lane (d = l % DW, i = l / DW) the values of
+// slices i, i + NI, ... (NI = 64 / DW interleaves).  Each wave forms every slice's weight itself
+// (lane s holds slice s: max, e^(m_s - M) and sum_s w_s l_s are wave reductions), so there is no
+// block barrier; the weights reach the value lanes through the wave's own LDS row.  The sums run
+// in the order of attention_combine_kernel (one round): the same bits.
+template <uint32_t DW>
+__global__ __launch_bounds__(256) void attention_combine_wave_kernel(const float *part, uint32_t q_heads,
+                                                                     uint32_t kv_heads, uint32_t D, uint32_t splits,
+                                                                     uint16_t *out) {
+    constexpr uint32_t NI = kWave / DW;
+    constexpr uint32_t J = kWave / NI;  // slices per lane at most
+    __shared__ float sw[4][kWave];
+    const uint32_t h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x & (kWave - 1);
+    const uint32_t w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t G = q_heads / kv_heads, kvh = h / G, g = h % G;
+    const size_t stride = (size_t)G * (D + 2);
+    const float *base = part + ((size_t)b * kv_heads + kvh) * splits * stride;
+    const uint32_t d = w * DW + lane % DW, il = lane / DW;
+    // all loads unconditional, from clamped slices (what they should not contribute is dropped below)
+    const uint32_t sl = min(lane, splits - 1);
+    const float mraw = base[sl * stride + g];
+    const float lraw = base[sl * stride + G + g];
+    float a[J];
+#pragma unroll
+    for (uint32_t j = 0; j < J; ++j) a[j] = base[min(il + NI * j, splits - 1) * stride + 2 * G + g * D + d];
+    const float mt = lane < splits ? mraw : -INFINITY;
+    float M = mt;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
+    const float wt = mt == -INFINITY ? 0.0f : expf(mt - M);
+    const float L = wave_sum(wt * (lane < splits ? lraw : 0.0f));
+    sw[w][lane] = wt;
+    __builtin_amdgcn_wave_barrier();
+    float acc = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < J; ++j) {
+        const uint32_t sj = il + NI * j;
+        if (sj < splits) acc = fmaf(sw[w][sj], a[j], acc);
+    }
+    float tot = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < NI; ++i) tot += __shfl(acc, (int)(lane % DW + i * DW));  // interleaves in order
+    if (il == 0) out[((size_t)b * q_heads + h) * D + d] = (uint16_t)f32_to_bf16(tot / L);
+}
+
 // One block (1024 threads) per row: index of the largest logit, ties to the
 // lowest index (NaN never wins).  Rows of n % 4 == 0 are read as float4,
 // eight loads in flight per thread.
@@ -712,8 +758,20 @@ hipError_t launch_rope_attention(const uint16_t *q, const uint16_t *k, const uin
 #undef KR_SPLIT
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(attention_combine_kernel, dim3(q_heads, batch), dim3(256), 0, s, part, q_heads, kv_heads, D,
-                       splits, out);
+    const dim3 mgrid(q_heads, batch);
+#define KR_MERGE(DW)                                                                                           \
+    hipLaunchKernelGGL(attention_combine_wave_kernel<DW>, mgrid, dim3(256), 0, s, part, q_heads, kv_heads, D, \
+                       splits, out)
+    const bool wave_merge = tuning().attn_merge_wave && splits <= kWave;
+    if (wave_merge && D == 256) KR_MERGE(64);
+    else if (wave_merge && D == 128) KR_MERGE(32);
+    else if (wave_merge && D == 64) KR_MERGE(16);
+    else if (wave_merge && D == 32) KR_MERGE(8);
+    else if (wave_merge && D == 16) KR_MERGE(4);
+    else if (wave_merge && D == 8) KR_MERGE(2);
+    else
+        hipLaunchKernelGGL(attention_combine_kernel, mgrid, dim3(256), 0, s, part, q_heads, kv_heads, D, splits, out);
+#undef KR_MERGE
     return hipGetLastError();
 }
 

@@ -270,6 +270,10 @@ int kr_set_option(int option, int value) {
             if (value != 0 && value != 1) return fail(KR_E_INVALID, "split-K tickets must be 0 or 1");
             tuning().splitk_tickets = value;
             return ok();
+        case KR_OPT_ATTN_MERGE_WAVE:
+            if (value != 0 && value != 1) return fail(KR_E_INVALID, "attention merge must be 0 or 1");
+            tuning().attn_merge_wave = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -288,6 +292,7 @@ int kr_get_option(int option) {
         case KR_OPT_MOE_GEMV: return tuning().moe_gemv;
         case KR_OPT_GEMV_LONG_GROUPS: return tuning().gemv_long_groups;
         case KR_OPT_SPLITK_TICKETS: return tuning().splitk_tickets;
+        case KR_OPT_ATTN_MERGE_WAVE: return tuning().attn_merge_wave;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }

@@ -39,6 +39,8 @@ struct Tuning {
                                        // MFMA kernel (0)
     int moe_gemv = 1;                  // MoE with <= 16 assignments: routed GEMV (1) or grouped MFMA kernel (0)
     int splitk_tickets = 1;            // few-token split K: 1 the last block of a run reduces, 0 a second launch
+    int attn_merge_wave = 1;           // decode attention merge of <= 64 slices, D a power of two 8..256:
+                                       // 1 the barrier-free wave kernel, 0 the general block kernel
 };
 Tuning &tuning();
 

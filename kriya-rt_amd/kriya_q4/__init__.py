@@ -34,6 +34,7 @@ OPT_GEMV_TOKENS = 9
 OPT_MOE_GEMV = 10
 OPT_GEMV_LONG_GROUPS = 11
 OPT_SPLITK_TICKETS = 12
+OPT_ATTN_MERGE_WAVE = 13
 
 _lib = None
 

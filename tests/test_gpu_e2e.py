@@ -152,6 +152,40 @@ def test_rope_attention_matches_two_step_path(kq, B, H, KVH, D, ctx, pos):
     assert np.all(np.abs(g - w) <= np.abs(w) * 2.0 ** -7 + 1e-3 * np.abs(w).max())
 
 
+@pytest.mark.parametrize("B,H,KVH,D,ctx,pos", [(2, 16, 2, 128, 513, [512, 130]), (1, 4, 4, 256, 1024, [1023]),
+                                               (2, 6, 1, 8, 20, [3, 19]), (1, 8, 2, 32, 40, [39]),
+                                               (1, 8, 2, 128, 1100, [1099])])
+def test_attention_merge_kernels_agree(kq, B, H, KVH, D, ctx, pos):
+    """The barrier-free merge (<= 64 slices, D a power of two) against the general merge kernel on the
+    same inputs: the same bits (they sum in the same order).  The last case has 69 slices, where
+    both settings run the general kernel."""
+    from kriya_q4 import synth
+    from kriya_q4.qwen_decode import rope_table
+    case(f"attention merge kernels B={B} H={H}/{KVH} D={D} ctx={ctx} pos={pos}")
+    q = dev_bf16(synth.bf16_normal((B, H * D), 3420))
+    k = dev_bf16(synth.bf16_normal((B, KVH * D), 3421))
+    v = dev_bf16(synth.bf16_normal((B, KVH * D), 3422))
+    kc0 = dev_bf16(synth.bf16_normal((B, ctx, KVH, D), 3423))
+    vc0 = dev_bf16(synth.bf16_normal((B, ctx, KVH, D), 3424))
+    cs = rope_table(ctx, D, 1e6).cuda()
+    posd = torch.tensor(pos, dtype=torch.int32).cuda()
+    outs = []
+    try:
+        for mode in (1, 0):
+            kq.set_option(kq.OPT_ATTN_MERGE_WAVE, mode)
+            kc, vc = kc0.clone(), vc0.clone()
+            outs.append(kq.rope_attention_decode(q, k, v, cs, posd, H, KVH, D, kc, vc).view(torch.int16).cpu())
+    finally:
+        kq.set_option(kq.OPT_ATTN_MERGE_WAVE, 1)
+    assert torch.equal(outs[0], outs[1])
+    qr = q.clone()
+    kc1, vc1 = kc0.clone(), vc0.clone()
+    kq.rope_kv_append(qr, k, v, cs, posd, H, KVH, D, kc1, vc1)
+    want = kq.attention_decode(qr, kc1, vc1, posd, H, KVH, D).float().cpu().numpy()
+    g = outs[0].view(torch.bfloat16).float().numpy()
+    assert np.all(np.abs(g - want) <= np.abs(want) * 2.0 ** -7 + 1e-3 * np.abs(want).max())
+
+
 @pytest.mark.parametrize("m", [1, 3, 9, 16])
 def test_rmsnorm_fused_qkv_and_mlp(kq, m):
     """qkv(rmsnorm(h)) and h += mlp(rmsnorm(h)) against kr_rmsnorm followed by the unfused calls:
