@@ -81,7 +81,8 @@ const char *kr_last_error(void);
                                            0 (default): only beyond k = 4096               */
 #define KR_OPT_GEMV_BLOCK_ROWS 4        /* rows per split-K block tile: 1, 2 (default), 4, 8 */
 #define KR_OPT_GEMV_PERSISTENT_BLOCKS 5 /* grid of the persistent wave kernel (1024)       */
-#define KR_OPT_SKINNY_MAX_BLOCKS 6      /* grid cap of the few-token kernel (512)          */
+#define KR_OPT_SKINNY_MAX_BLOCKS 6      /* grid cap of the few-token kernel (256; grouped
+                                           MoE launches take twice this)                  */
 #define KR_OPT_PREFILL_KERNEL 7         /* m > 16: 0 register-dequant (default), 1 tiled, 2 register-dequant
                                            with 64-column steps (0 takes 128 where k allows) */
 #define KR_OPT_GEMV_LONG_ROWS 8         /* k > 4096 rows per long-row block: 4, 8 (default), 16; 0 split-K */

@@ -29,7 +29,8 @@ struct Tuning {
     int gemv_persistent_blocks = 1024; // grid of the persistent wave kernel
     int gemv_split_k_chunks = 0;       // rows of >= this many 16-byte chunks use the block kernel
                                        // (always beyond 128 chunks); 0 = default
-    int skinny_max_blocks = 512;       // grid cap of the few-token kernel (blocks walk runs of tiles)
+    int skinny_max_blocks = 256;       // grid cap of the few-token kernel (blocks walk runs of tiles);
+                                       // grouped MoE launches take twice this
     int prefill_kernel = 0;            // m > 16: 0 = register-dequant prefill kernel,
                                        // 1 = LDS-dequant tiled kernel
     int gemv_long_rows = 8;            // k > 4096: rows per block of the long-row kernels (4, 8, 16);
