@@ -565,11 +565,14 @@ __global__ __launch_bounds__(256) void attention_combine_kernel(const float *par
         const float wt = mt == -INFINITY ? 0.0f : expf(mt - Mc);
         sw[tid] = wt;
         const float Lr = block_sum256(wt * lt, r4);  // also publishes sw
+        // A slice with weight 0 is skipped, not multiplied: an empty slice (past the sequence) writes
+        // only its (m, l), so its acc holds whatever the workspace held (possibly NaN or inf).
+        // Skipping leaves finite sums bit-identical (fmaf(0, a, acc) == acc).
         float part_acc = 0.0f;
 #pragma unroll
         for (uint32_t j = 0; j < kPer; ++j) {
             const uint32_t sj = il + j * NI;
-            if (il < NI && sj < cnt) part_acc = fmaf(sw[sj], a[j], part_acc);
+            if (il < NI && sj < cnt && sw[sj] != 0.0f) part_acc = fmaf(sw[sj], a[j], part_acc);
         }
         if (il < NI) red[tid] = part_acc;
         __syncthreads();
@@ -620,9 +623,9 @@ __global__ __launch_bounds__(256) void attention_combine_wave_kernel(const float
     __builtin_amdgcn_wave_barrier();
     float acc = 0.0f;
 #pragma unroll
-    for (uint32_t j = 0; j < J; ++j) {
+    for (uint32_t j = 0; j < J; ++j) {  // weight-0 slices skipped, as in attention_combine_kernel
         const uint32_t sj = il + NI * j;
-        if (sj < splits) acc = fmaf(sw[w][sj], a[j], acc);
+        if (sj < splits && sw[w][sj] != 0.0f) acc = fmaf(sw[w][sj], a[j], acc);
     }
     float tot = 0.0f;
 #pragma unroll

@@ -397,8 +397,11 @@ __global__ __launch_bounds__(256) void q4_moe_gemv_kernel(MoeGemvArgs a) {
         // sorted[p] through a lane-varying zero: a uniform load is moved to a scalar register
         // right away (a wait before the expert lookup is even requested); this one stays in a
         // vector register until its use
-        const uint32_t sp = a.sorted[p + __builtin_amdgcn_mbcnt_lo(0u, 0u)];
-        const uint32_t e = expert_of(p);
+        // Both are clamped: a position at or past offsets[E] (an id >= E that joined no bucket)
+        // has no expert and an unwritten sorted[p].  Its rows are then some expert's result for
+        // some assignment (unspecified), but every access stays inside the arrays.
+        const uint32_t sp = min(a.sorted[p + __builtin_amdgcn_mbcnt_lo(0u, 0u)], a.assign - 1);
+        const uint32_t e = min(expert_of(p), a.experts - 1);
         const size_t r0 = (size_t)e * a.rows;
         A.qw = a.w.qw + r0 * wpr;
         A.sc = a.w.sc + r0 * groups;

@@ -225,12 +225,15 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         const bool ok = eout && ef < crows;
         const uint16_t *bsrc = (cbias && ok) ? cbias + (size_t)e * crows + ef : a.x;
         pre_b[b] = *bsrc;
-        // old output: one aligned u32 (a bf16 output reads the pair holding it)
+        // old output: an f32 or a bf16 load of exactly the element (both issued, from x when
+        // unused, so that no branch holds them up; a 32-bit read of a bf16 pair could pass the end)
         const size_t o = (size_t)orow * cldo + ef;
-        const uint32_t *osrc = a.out_f32 ? reinterpret_cast<const uint32_t *>(cout) + o
-                                         : reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(cout) +
-                                                                              (o & ~(size_t)1));
-        pre_o[b] = *((a.accumulate && ok) ? osrc : reinterpret_cast<const uint32_t *>(a.x));
+        const bool acc_ok = a.accumulate && ok;
+        const uint32_t *o32 = (acc_ok && a.out_f32) ? reinterpret_cast<const uint32_t *>(cout) + o
+                                                    : reinterpret_cast<const uint32_t *>(a.x);
+        const uint16_t *o16 = (acc_ok && !a.out_f32) ? reinterpret_cast<const uint16_t *>(cout) + o : a.x;
+        const uint32_t v32 = *o32, v16 = *o16;
+        pre_o[b] = a.out_f32 ? v32 : v16;
     };
     // The words (and scale/bias pairs) of tile t.
     auto fetch_words = [&](auto BUF, uint32_t e, uint32_t t) {
@@ -431,7 +434,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
                 if (a.out_f32) {
                     reinterpret_cast<float *>(cout)[o] = a.accumulate ? __uint_as_float(pre_o[b]) + val : val;
                 } else {
-                    const uint32_t old = (o & 1) ? pre_o[b] >> 16 : pre_o[b] & 0xFFFFu;
+                    const uint32_t old = pre_o[b] & 0xFFFFu;
                     reinterpret_cast<uint16_t *>(cout)[o] =
                         (uint16_t)f32_to_bf16(a.accumulate ? val + bf16_to_f32(old) : val);
                 }
@@ -471,6 +474,17 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         __syncthreads();
         uint32_t *s_ticket = reinterpret_cast<uint32_t *>(&red[0][0][0][0]);  // red is free here
         const uint32_t rb = blockIdx.x / a.ksplit;
+        // Ordering argument (a hardware one, not a C++ release/acquire pair).  The partials were
+        // written with agent-scope relaxed atomic stores: on gfx950 these are global stores with
+        // the sc1 cache policy, written through this XCD's L2 to the device-coherent level.  The
+        // s_waitcnt vmcnt(0) above returns only once every such store is acknowledged at that
+        // level, and the barrier orders all threads' waits before this ticket.  The reducer reads
+        // the partials with agent-scope relaxed atomic loads (sc1: never served from a stale
+        // non-coherent cache line), issued after its ticket came back.  A release/acquire pair at
+        // agent scope would add an L2 write-back (buffer_wbl2) on every block and an invalidate on
+        // the reducers: the MLP step at m = 16 took 126 us that way against 27 us.  If the store
+        // path changes, KR_OPT_SPLITK_TICKETS = 0 (a second reduction launch, ordered by the
+        // stream) is the fallback; tests compare the two bit for bit.
         if (tid == 0) s_ticket[0] = atomicAdd(&a.tickets[rb], 1u);
         __syncthreads();
         if (s_ticket[0] != a.ksplit - 1) return;

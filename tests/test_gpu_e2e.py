@@ -186,6 +186,37 @@ def test_attention_merge_kernels_agree(kq, B, H, KVH, D, ctx, pos):
     assert np.all(np.abs(g - want) <= np.abs(want) * 2.0 ** -7 + 1e-3 * np.abs(want).max())
 
 
+@pytest.mark.parametrize("merge_wave", [1, 0])
+@pytest.mark.parametrize("B,H,KVH,D,ctx,pos", [(2, 16, 2, 128, 513, [130, 7]), (1, 8, 2, 64, 1100, [40])])
+def test_attention_workspace_garbage_in_empty_slices(kq, merge_wave, B, H, KVH, D, ctx, pos):
+    """Slices past a sequence's length write only their (m, l); the merge must not read their
+    partial sums.  The workspace is filled with 0xFF bytes (f32 NaN) before the call, and the result
+    must equal the one from a zeroed workspace bit for bit.  ctx 1100 has 69 slices (general merge)."""
+    from kriya_q4 import synth
+    from kriya_q4.qwen_decode import rope_table
+    case(f"attention, NaN-filled workspace, merge_wave={merge_wave} B={B} ctx={ctx} pos={pos}")
+    q = dev_bf16(synth.bf16_normal((B, H * D), 3430))
+    k = dev_bf16(synth.bf16_normal((B, KVH * D), 3431))
+    v = dev_bf16(synth.bf16_normal((B, KVH * D), 3432))
+    kc0 = dev_bf16(synth.bf16_normal((B, ctx, KVH, D), 3433))
+    vc0 = dev_bf16(synth.bf16_normal((B, ctx, KVH, D), 3434))
+    cs = rope_table(ctx, D, 1e6).cuda()
+    posd = torch.tensor(pos, dtype=torch.int32).cuda()
+    outs = []
+    try:
+        kq.set_option(kq.OPT_ATTN_MERGE_WAVE, merge_wave)
+        for fill in (0x00, 0xFF):
+            ws = kq.attention_workspace(B, H, D, ctx)
+            ws.fill_(fill)
+            kc, vc = kc0.clone(), vc0.clone()
+            out = kq.rope_attention_decode(q, k, v, cs, posd, H, KVH, D, kc, vc, workspace=ws)
+            outs.append(out.view(torch.int16).cpu())
+    finally:
+        kq.set_option(kq.OPT_ATTN_MERGE_WAVE, 1)
+    assert torch.isfinite(outs[1].view(torch.bfloat16).float()).all()
+    assert torch.equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("m", [1, 3, 9, 16])
 def test_rmsnorm_fused_qkv_and_mlp(kq, m):
     """qkv(rmsnorm(h)) and h += mlp(rmsnorm(h)) against kr_rmsnorm followed by the unfused calls:

@@ -59,6 +59,22 @@ def test_linear_batched_shapes(kq, m, n, k):
     assert_bf16_rounded_close(host_bits(r), O.bf16_to_f32(r0) + want, rms(want), what=f"acc m={m}")
 
 
+@pytest.mark.parametrize("m,n", [(3, 77), (5, 77), (9, 33), (17, 45)])
+def test_linear_accumulate_bf16_odd_element_count(kq, m, n):
+    """bf16 accumulate where m * n is odd: the last element has no partner in a 32-bit pair, so the
+    epilogue must read exactly the element it updates (the output tensor ends right after it)."""
+    s = synth()
+    k = 256
+    case(f"bf16 accumulate, odd element count m={m} n={n}")
+    wq = s.q4_weight(n, k, 3300 + m + n)
+    x = s.bf16_normal((m, k), 3310 + m)
+    want = O.q4_matmul(O.Q4Planar(*wq), x)
+    r0 = s.bf16_normal((m, n), 3320 + m)
+    r = dev_bf16(r0).clone()
+    kq.q4_linear(q4_dev(kq, wq), dev_bf16(x), y=r, accumulate=True)
+    assert_bf16_rounded_close(host_bits(r), O.bf16_to_f32(r0) + want, rms(want), what=f"acc m={m} n={n}")
+
+
 CFG2 = [("q", 2048, 2048, 2001), ("k", 256, 2048, 2002), ("v", 256, 2048, 2003), ("o", 2048, 2048, 2004),
         ("gate", 11008, 2048, 2005), ("up", 11008, 2048, 2006), ("down", 2048, 11008, 2007)]
 

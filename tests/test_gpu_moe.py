@@ -184,6 +184,36 @@ def test_moe_config4(kq, T):
     assert_rms_close(y, want, what=f"cfg4 T={T}")
 
 
+def test_moe_experts_with_an_unbucketed_assignment(kq):
+    """Routing from scan/scatter with an id >= E leaves offsets[E] < T * K and the tail of the sorted
+    list unwritten (here: filled with 0xFFFFFFFF).  The header leaves the outputs unspecified; the
+    kernels clamp the expert and the sorted entry, so the call completes with finite outputs."""
+    T, E, K, H, I = 2, 4, 2, 256, 128
+    case("moe experts, one assignment with an out-of-range expert id")
+    s = synth()
+    g, u = s.q4_weight(E * I, H, 4701), s.q4_weight(E * I, H, 4702)
+    d = s.q4_weight(E * H, I, 4703)
+    x = s.bf16_normal((T, H), 4704)
+    sel = np.array([1, 0, 9, 3], np.uint32)
+    counts, offsets, scatter = kq.moe_scan_scatter(i32(sel), E)
+    assert int(offsets[E].item()) == 3
+    r = kq.MoeRoute(T, E, K)
+    r.selected.copy_(i32(sel).view(T, K))
+    r.weights.fill_(0.5)
+    r.counts.copy_(counts)
+    r.offsets.copy_(offsets)
+    r.sorted_assign.fill_(-1)
+    r.sorted_assign[:3].copy_(scatter[:3])
+    for gemv in (1, 0):
+        kq.set_option(kq.OPT_MOE_GEMV, gemv)
+        try:
+            y = kq.moe_experts(q4_dev(kq, g), q4_dev(kq, u), q4_dev(kq, d), E, dev_bf16(x), r)
+            torch.cuda.synchronize()
+        finally:
+            kq.set_option(kq.OPT_MOE_GEMV, 1)
+        assert torch.isfinite(y).all()
+
+
 def test_moe_crowded_experts(kq):
     """More than 16 tokens per expert: the 16-row chunk loop."""
     T, E, K, H, I = 40, 12, 2, 256, 128
