@@ -15,7 +15,8 @@
  *     that fails a check enqueues nothing.  (The reference performs no shape
  *     checks in its encode functions, encoder.rs:2361-2536.)
  *   - Calls on distinct streams are independent; the library keeps no
- *     per-call state on the device.
+ *     per-call state on the device (except kr_q4_mlp_noalloc, whose device
+ *     scratch array is shared by every call on one GPU).
  *   - Results do not depend on the launch grid: every output element is
  *     reduced by one wavefront in a fixed order (no atomics on data).
  *
@@ -191,6 +192,22 @@ int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matr
               const uint16_t *x, void *h, int h_dtype, uint32_t m, int activation,
               void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- dense MLP without a workspace (no counterpart in the reference, whose
+ *      executor pre-allocates its scratch buffers, encoder.rs:1957-2035) ----
+ * For callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  Same arguments, results
+ * and kernels as kr_q4_mlp, but the workspace is a device array inside the
+ * library: kr_q4_mlp_noalloc_max_bytes() (4 MiB) on each GPU, held until the
+ * process ends.  A call whose kr_q4_mlp_workspace_bytes(m, hidden, inter)
+ * exceeds it fails with KR_E_WORKSPACE and enqueues nothing (cfg-1 shape
+ * hidden 2048, inter 11008: m <= 37).  Allocates nothing, on the device or the
+ * host.  The first call on a device also enqueues a small kernel that zeroes
+ * the array's split-K counters.  All calls on one GPU share its array: calls
+ * that overlap in time on one GPU (other streams, other threads) race. */
+size_t kr_q4_mlp_noalloc_max_bytes(void);
+int kr_q4_mlp_noalloc(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down,
+                      const uint16_t *x, void *h, int h_dtype, uint32_t m, int activation, void *stream);
+
 /* ---- MoE routing: q4_gemm_and_moe.metal:2495-2624 (moe_router_topk_and_histogram
  *      + moe_router_prefix_scan_and_scatter, dispatched at encoder.rs:5275-5313) ----
  * logits: f32 [tokens, experts].  Per token: softmax, then the top `topk`
@@ -230,7 +247,10 @@ int kr_moe_scan_scatter(const uint32_t *selected, uint32_t num_assign, uint32_t 
  * shared expert (moe_combine_routed_and_shared_bf16 with has_shared_expert,
  * transformer_glue.metal:396-398) is this form with y holding the shared
  * expert's bf16 output: the routed sum, then + shared, rounded once to bf16.
- * offsets and sorted_assign are kr_moe_route's.  Every expert's weights are read
+ * offsets and sorted_assign are kr_moe_route's: every assignment in a bucket,
+ * offsets[experts] == tokens * topk.  Routing from kr_moe_scan_scatter with ids
+ * >= experts breaks that; then the outputs are unspecified, but every memory
+ * access stays inside the given arrays.  Every expert's weights are read
  * once per call for all the tokens routed to it (grouped matmul; the reference
  * re-reads them per routed token).  The reference also rounds gate.x, up.x and
  * d_a to bf16; here they stay f32.

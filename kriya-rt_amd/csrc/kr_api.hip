@@ -7,6 +7,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 #include "kriya_glue.h"
@@ -844,6 +845,73 @@ int kr_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, voi
     if (n == 0) return fail(KR_E_SHAPE, "n must be positive");
     if (!aligned(logits, 4) || !aligned(out, 4)) return fail(KR_E_ALIGN, "logits/out misaligned");
     return hip_status(launch_argmax(logits, rows, n, out, (hipStream_t)stream), "kr_argmax");
+}
+
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- kr_q4_mlp_noalloc
+// kr_q4_mlp for callers that cannot allocate device memory (code under HIP graph
+// capture, serving loops, harnesses that forbid hipMalloc): the workspace is the file-scope
+// device array `scratch`, one copy per GPU, held until the process ends.  Its device address
+// is taken once per device with hipGetSymbolAddress; the host never passes the array's own
+// name to a kernel or a copy.  The kernels are kr_q4_mlp's.
+
+namespace {
+
+constexpr size_t kMlpScratchBytes = (size_t)4 << 20;  // 4 MiB per GPU
+__device__ __align__(256) unsigned char scratch[kMlpScratchBytes];
+
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchMaxDevices];  // device address of `scratch` on each device, once set up
+
+__global__ void zero_words_kernel(uint32_t *p, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// The scratch address on the current device.  The first call on a device takes the address and
+// enqueues a fill kernel on `s` that zeroes the split-K tickets (every call leaves them zero
+// after that); a kernel, not hipMemsetAsync, so that a first call under graph capture records a
+// plain kernel node.
+int scratch_on_current_device(hipStream_t s, void **out) {
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev)) return hip_status(e, "kr_q4_mlp_noalloc: hipGetDevice");
+    if (dev < 0 || dev >= kScratchMaxDevices) return fail(KR_E_UNSUPPORTED, "kr_q4_mlp_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)))
+            return hip_status(e, "kr_q4_mlp_noalloc: hipGetSymbolAddress(scratch)");
+        const uint32_t words = (uint32_t)(kMlpTicketBytes / 4);
+        hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, s, (uint32_t *)p, words);
+        if (hipError_t e = hipGetLastError()) return hip_status(e, "kr_q4_mlp_noalloc: clearing the tickets");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return KR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t kr_q4_mlp_noalloc_max_bytes(void) { return kMlpScratchBytes; }
+
+int kr_q4_mlp_noalloc(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, const uint16_t *x,
+                      void *h, int h_dtype, uint32_t m, int activation, void *stream) {
+    if (int rc = check_matrix(gate, "gate")) return rc;
+    const size_t need = kr_q4_mlp_workspace_bytes(m, gate->k, gate->n);
+    if (need > kMlpScratchBytes)
+        return fail(KR_E_WORKSPACE,
+                    "kr_q4_mlp_noalloc: m=%u hidden=%u intermediate=%u needs %zu bytes of scratch, more than the "
+                    "%zu the library holds per GPU; call kr_q4_mlp with a workspace",
+                    m, gate->k, gate->n, need, kMlpScratchBytes);
+    if (m == 0) return kr_q4_mlp(gate, up, down, x, h, h_dtype, m, activation, nullptr, 0, stream);
+    void *ws = nullptr;
+    if (int rc = scratch_on_current_device((hipStream_t)stream, &ws)) return rc;
+    return kr_q4_mlp(gate, up, down, x, h, h_dtype, m, activation, ws, kMlpScratchBytes, stream);
 }
 
 }  // extern "C"

@@ -81,6 +81,8 @@ def lib():
             "kr_q4_mlp_workspace_bytes": (sz, [u32, u32, u32]),
             "kr_q4_qkv": (i32, [M, M, M, vp, vp, vp, vp, u32, vp, vp, vp, i32, vp]),
             "kr_q4_mlp": (i32, [M, M, M, vp, vp, i32, u32, i32, vp, sz, vp]),
+            "kr_q4_mlp_noalloc_max_bytes": (sz, []),
+            "kr_q4_mlp_noalloc": (i32, [M, M, M, vp, vp, i32, u32, i32, vp]),
             "kr_moe_route": (i32, [vp, u32, u32, u32, i32, vp, vp, vp, vp, vp, vp]),
             "kr_moe_scan_scatter": (i32, [vp, u32, u32, vp, vp, vp, vp]),
             "kr_q4_moe_workspace_bytes": (sz, [u32, u32, u32, u32]),
@@ -272,6 +274,16 @@ def mlp(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, h: torch.Tensor, x: Option
         workspace = mlp_workspace(m, gate.k, gate.n, device=h.device)
     _check(lib().kr_q4_mlp(gate.desc, up.desc, down.desc, _ptr(x), _ptr(h), _dt_of(h), m, activation,
                            _ptr(workspace), workspace.numel(), _stream(stream)))
+    return h
+
+
+def mlp_noalloc(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, h: torch.Tensor, x: Optional[torch.Tensor] = None,
+                activation: int = ACT_SWIGLU, stream=None) -> torch.Tensor:
+    """mlp() with the library's own per-GPU scratch as the workspace (kr_q4_mlp_noalloc): nothing is
+    allocated; calls that overlap on one GPU race."""
+    m = h.numel() // down.n
+    _check(lib().kr_q4_mlp_noalloc(gate.desc, up.desc, down.desc, _ptr(x), _ptr(h), _dt_of(h), m, activation,
+                                   _stream(stream)))
     return h
 
 

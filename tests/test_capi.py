@@ -129,3 +129,16 @@ def test_moe_argument_checks(kq):
     assert L.kr_q4_moe_experts(*(ctypes.byref(w) for w in wide), E, *args) == kq.KR_E_UNSUPPORTED
     odd = _mat(kq, n=E * 192, k=H), _mat(kq, n=E * 192, k=H), _mat(kq, n=E * H, k=192)
     assert L.kr_q4_moe_experts(*(ctypes.byref(w) for w in odd), E, *args) == kq.KR_E_UNSUPPORTED
+
+
+def test_mlp_noalloc_rejects_sizes_beyond_its_scratch(kq):
+    """kr_q4_mlp_noalloc checks its need against the library's per-GPU scratch before any HIP call."""
+    L = kq.lib()
+    assert L.kr_q4_mlp_noalloc_max_bytes() == 4 << 20
+    g, u = _mat(kq, n=11008, k=2048), _mat(kq, n=11008, k=2048)
+    d = _mat(kq, n=2048, k=11008)
+    h = 0x40000
+    rc = L.kr_q4_mlp_noalloc(ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), None, h, kq.DTYPE_BF16, 64, 0, None)
+    assert rc == kq.KR_E_WORKSPACE
+    assert b"kr_q4_mlp_noalloc" in L.kr_last_error() and b"kr_q4_mlp with a workspace" in L.kr_last_error()
+    assert L.kr_q4_mlp_workspace_bytes(37, 2048, 11008) <= 4 << 20 < L.kr_q4_mlp_workspace_bytes(38, 2048, 11008)
