@@ -265,6 +265,26 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
                       int activation, void *y, int y_dtype, int accumulate,
                       void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- the whole routed MoE stage on the device: the SparseMoE channel mixer of
+ *      forward_and_sample_impl / forward_prefill_batch (encoder.rs:5246-5445 and
+ *      4425-4625): router Q4 GEMV -> top-k routing -> experts -> combine ----
+ * logits = x . router^T in f32 (router: Q4 [experts, hidden]), then
+ * kr_moe_route(logits, normalize) and kr_q4_moe_experts(...) as above, all on
+ * `stream` with nothing returned to the host.  The reference writes the router
+ * logits as bf16 and reads them as f32, and never resets its expert counters
+ * (encoder.rs:4435-4445, 5255-5265, 1982); here the logits stay f32 and the
+ * routing keeps no state between calls.
+ * x: bf16 [tokens, hidden] (the normed hidden state); y as kr_q4_moe_experts'.
+ * workspace: kr_q4_moe_block_workspace_bytes(tokens, experts, topk, hidden, inter)
+ * bytes, 16-byte aligned; calls sharing it must not overlap in time.
+ * Limits: those of kr_moe_route and kr_q4_moe_experts. */
+size_t kr_q4_moe_block_workspace_bytes(uint32_t tokens, uint32_t experts, uint32_t topk, uint32_t hidden,
+                                       uint32_t inter);
+int kr_q4_moe_block(const kr_q4_matrix *router, const kr_q4_matrix *gate, const kr_q4_matrix *up,
+                    const kr_q4_matrix *down, uint32_t experts, const uint16_t *x, uint32_t tokens, uint32_t topk,
+                    int normalize, int activation, void *y, int y_dtype, int accumulate, void *workspace,
+                    size_t workspace_bytes, void *stream);
+
 /* ---- Q4 embedding lookup: transformer_glue.metal:122-152 (embedding_lookup_q4_g64),
  *      dispatched at encoder.rs:4803-4846 ----
  * out[t, :] = bf16(fma(q, s, b)) of row tokens[t] of w (the tied Q4 embedding

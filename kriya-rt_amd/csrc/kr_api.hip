@@ -674,6 +674,87 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
                       "kr_q4_moe_experts (combine)");
 }
 
+// kr_q4_moe_block workspace: router logits f32 [T, E], selected u32 [T*K], weights f32 [T*K],
+// counts u32 [E], offsets u32 [E+1], sorted u32 [T*K], then the experts' workspace.
+namespace {
+struct MoeBlockLayout {
+    size_t logits, selected, weights, counts, offsets, sorted, experts, total;
+};
+MoeBlockLayout moe_block_layout(uint32_t tokens, uint32_t experts, uint32_t topk, uint32_t hidden, uint32_t inter) {
+    const size_t assign = (size_t)tokens * topk;
+    MoeBlockLayout L{};
+    size_t o = 0;
+    L.logits = o;   o += round_up((size_t)tokens * experts * 4, 256);
+    L.selected = o; o += round_up(std::max<size_t>(assign, 1) * 4, 256);
+    L.weights = o;  o += round_up(std::max<size_t>(assign, 1) * 4, 256);
+    L.counts = o;   o += round_up((size_t)experts * 4, 256);
+    L.offsets = o;  o += round_up(((size_t)experts + 1) * 4, 256);
+    L.sorted = o;   o += round_up(std::max<size_t>(assign, 1) * 4, 256);
+    L.experts = o;  o += kr_q4_moe_workspace_bytes(tokens, topk, hidden, inter);
+    L.total = o;
+    return L;
+}
+}  // namespace
+
+size_t kr_q4_moe_block_workspace_bytes(uint32_t tokens, uint32_t experts, uint32_t topk, uint32_t hidden,
+                                       uint32_t inter) {
+    return moe_block_layout(tokens, experts, topk, hidden, inter).total;
+}
+
+int kr_q4_moe_block(const kr_q4_matrix *router, const kr_q4_matrix *gate, const kr_q4_matrix *up,
+                    const kr_q4_matrix *down, uint32_t experts, const uint16_t *x, uint32_t tokens, uint32_t topk,
+                    int normalize, int activation, void *y, int y_dtype, int accumulate, void *workspace,
+                    size_t workspace_bytes, void *stream) {
+    if (int rc = check_matrix(router, "router")) return rc;
+    if (int rc = check_matrix(gate, "gate")) return rc;
+    if (experts == 0 || experts > kMaxExperts) return fail(KR_E_INVALID, "experts=%u must be in 1..%u", experts, kMaxExperts);
+    if (router->n != experts || router->k != gate->k)
+        return fail(KR_E_SHAPE, "router [%u,%u] must be [experts=%u, hidden=%u]", router->n, router->k, experts, gate->k);
+    if (gate->n % experts != 0) return fail(KR_E_SHAPE, "gate rows %u are not a multiple of experts=%u", gate->n, experts);
+    // every check of the three stages before the first launch: a failing call enqueues nothing
+    if (int rc = check_matrix(up, "up")) return rc;
+    if (int rc = check_matrix(down, "down")) return rc;
+    const uint32_t hidden = gate->k, inter = gate->n / experts;
+    if (up->n != gate->n || up->k != hidden) return fail(KR_E_SHAPE, "gate and up shapes differ");
+    if (down->k != inter || down->n != experts * hidden)
+        return fail(KR_E_SHAPE, "down [%u,%u] does not stack %u experts of [%u,%u]", down->n, down->k, experts, hidden,
+                    inter);
+    if (!skinny_grouped_fits(hidden) || !skinny_grouped_fits(inter))
+        return fail(KR_E_UNSUPPORTED, "hidden=%u / inter=%u: need multiples of 128 up to 2048", hidden, inter);
+    if (!skinny_supported(to_mat(gate)) || !skinny_supported(to_mat(up)) || !skinny_supported(to_mat(down)))
+        return fail(KR_E_ALIGN, "expert scales/biases must be 4-byte aligned");
+    if (topk == 0 || topk > experts || topk > kRouteMaxTopK)
+        return fail(KR_E_INVALID, "topk=%u must be in 1..min(experts, %u)", topk, kRouteMaxTopK);
+    if (!valid_dtype(y_dtype)) return fail(KR_E_INVALID, "y_dtype %d invalid", y_dtype);
+    if (!valid_act(activation)) return fail(KR_E_INVALID, "activation %d invalid", activation);
+    if (accumulate != 0 && accumulate != 1) return fail(KR_E_INVALID, "accumulate must be 0 or 1");
+    if (tokens == 0) return ok();
+    if ((uint64_t)tokens * topk > kRouteMaxAssign)
+        return fail(KR_E_SHAPE, "tokens * topk = %llu exceeds %u", (unsigned long long)tokens * topk, kRouteMaxAssign);
+    if (!x || !y) return fail(KR_E_INVALID, "x/y must be non-NULL");
+    if (!aligned(x, 16)) return fail(KR_E_ALIGN, "x must be 16-byte aligned");
+    if (!aligned(y, dtype_size(y_dtype) * 4)) return fail(KR_E_ALIGN, "y must be aligned to 4 elements");
+    const MoeBlockLayout L = moe_block_layout(tokens, experts, topk, hidden, inter);
+    if (!workspace || workspace_bytes < L.total)
+        return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", L.total, workspace_bytes);
+    if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
+    char *ws = (char *)workspace;
+    float *logits = (float *)(ws + L.logits);
+    uint32_t *selected = (uint32_t *)(ws + L.selected);
+    float *weights = (float *)(ws + L.weights);
+    uint32_t *counts = (uint32_t *)(ws + L.counts), *offsets = (uint32_t *)(ws + L.offsets);
+    uint32_t *sorted = (uint32_t *)(ws + L.sorted);
+    // 1. router logits in f32 (the reference stores them as bf16 and reads them as f32)
+    if (int rc = kr_q4_linear(router, x, tokens, logits, KR_DTYPE_F32, 0, stream)) return rc;
+    // 2. softmax, top-k, renormalisation, deterministic buckets
+    if (int rc = kr_moe_route(logits, tokens, experts, topk, normalize, selected, weights, counts, offsets, sorted,
+                              stream))
+        return rc;
+    // 3. experts (gate/up + activation, down) and the weighted combine into y
+    return kr_q4_moe_experts(gate, up, down, experts, x, tokens, topk, weights, offsets, sorted, activation, y, y_dtype,
+                             accumulate, ws + L.experts, L.total - L.experts, stream);
+}
+
 int kr_q4_embedding(const kr_q4_matrix *w, const uint32_t *tokens, uint32_t count, uint16_t *out, void *stream) {
     if (int rc = check_matrix(w, "w")) return rc;
     if (count == 0) return ok();

@@ -87,6 +87,8 @@ def lib():
             "kr_moe_scan_scatter": (i32, [vp, u32, u32, vp, vp, vp, vp]),
             "kr_q4_moe_workspace_bytes": (sz, [u32, u32, u32, u32]),
             "kr_q4_moe_experts": (i32, [M, M, M, u32, vp, u32, u32, vp, vp, vp, i32, vp, i32, i32, vp, sz, vp]),
+            "kr_q4_moe_block_workspace_bytes": (sz, [u32, u32, u32, u32, u32]),
+            "kr_q4_moe_block": (i32, [M, M, M, M, u32, vp, u32, u32, i32, i32, vp, i32, i32, vp, sz, vp]),
             "kr_q4_embedding": (i32, [M, vp, u32, vp, vp]),
             "kr_rmsnorm": (i32, [vp, vp, u32, u32, ctypes.c_float, vp, vp]),
             "kr_rope_kv_append": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, u32, vp]),
@@ -374,6 +376,27 @@ def moe_experts(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, experts: int, x: t
                                    _ptr(route.weights), _ptr(route.offsets), _ptr(route.sorted_assign), activation,
                                    _ptr(y), _dt_of(y), int(accumulate), _ptr(workspace), workspace.numel(),
                                    _stream(stream)))
+    return y
+
+
+def moe_block_workspace(tokens: int, experts: int, topk: int, hidden: int, inter: int, device="cuda") -> torch.Tensor:
+    nbytes = int(lib().kr_q4_moe_block_workspace_bytes(tokens, experts, topk, hidden, inter))
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def moe_block(router: Q4Matrix, gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, experts: int, x: torch.Tensor,
+              topk: int, normalize: bool = True, y: Optional[torch.Tensor] = None, out_dtype: int = DTYPE_F32,
+              accumulate: bool = False, activation: int = ACT_SWIGLU, workspace: Optional[torch.Tensor] = None,
+              stream=None) -> torch.Tensor:
+    """The routed MoE stage on the device: f32 router logits (Q4 GEMV) -> routing -> experts -> combine."""
+    tokens = x.numel() // gate.k
+    if y is None:
+        y = torch.zeros((tokens, gate.k), dtype=_out_dtype(out_dtype), device=x.device)
+    if workspace is None:
+        workspace = moe_block_workspace(tokens, experts, topk, gate.k, gate.n // experts, device=x.device)
+    _check(lib().kr_q4_moe_block(router.desc, gate.desc, up.desc, down.desc, experts, _ptr(x), tokens, topk,
+                                 int(normalize), activation, _ptr(y), _dt_of(y), int(accumulate), _ptr(workspace),
+                                 workspace.numel(), _stream(stream)))
     return y
 
 

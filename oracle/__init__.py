@@ -70,6 +70,7 @@ def _declare(L):
     W = [_u32p, _u16p, _u16p]
     L.kro_q4_matmul.argtypes = W + [ctypes.c_uint32, ctypes.c_uint32, _u16p, ctypes.c_uint32, _f32p, ctypes.c_int]
     L.kro_q4_matmul_f64.argtypes = W + [ctypes.c_uint32, ctypes.c_uint32, _u16p, ctypes.c_uint32, _f64p, ctypes.c_int]
+    L.kro_f32_matmul.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, _f32p, ctypes.c_uint32, _f32p, ctypes.c_int]
     L.kro_activation.restype = ctypes.c_float
     L.kro_activation.argtypes = [ctypes.c_float, ctypes.c_int]
     L.kro_q4_gate_up_act.argtypes = W + W + [ctypes.c_uint32, ctypes.c_uint32, _u16p, ctypes.c_uint32,
@@ -240,6 +241,17 @@ def q4_matmul_f64(w: Q4Planar, x_bf16: np.ndarray, threads: int | None = None) -
     y = np.empty((m, w.n), np.float64)
     lib().kro_q4_matmul_f64(*w.ptrs(), w.n, w.k, _p(x, ctypes.c_uint16), m, _p(y, ctypes.c_double),
                             threads or default_threads())
+    return y
+
+
+def f32_matmul(w_f32: np.ndarray, x_f32: np.ndarray, threads: int | None = None) -> np.ndarray:
+    """Y[m, n] = sequential f32 dot of pre-dequantised rows w [n, k] with x [m, k] (f32)."""
+    w = np.ascontiguousarray(w_f32, dtype=np.float32)
+    n, k = w.shape
+    x = np.ascontiguousarray(x_f32, dtype=np.float32).reshape(-1, k)
+    y = np.empty((x.shape[0], n), np.float32)
+    lib().kro_f32_matmul(_p(w, ctypes.c_float), n, k, _p(x, ctypes.c_float), x.shape[0], _p(y, ctypes.c_float),
+                         threads or default_threads())
     return y
 
 

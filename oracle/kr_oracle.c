@@ -299,6 +299,31 @@ static void matmul_f32x(const uint32_t *qw, const uint16_t *sc, const uint16_t *
     parallel_for(n, nthreads, mm_range, &c);
 }
 
+/* The CPU baseline's upper bound: the same sequential f32 dot on weights that were
+ * dequantised once beforehand (w f32 [n, k]), so only the dot products are timed. */
+typedef struct { const float *w; uint32_t n, k, m; const float *x; float *y; } f32mm_ctx;
+
+static void f32mm_range(void *p, size_t begin, size_t end) {
+    f32mm_ctx *c = (f32mm_ctx *)p;
+    for (size_t r = begin; r < end; ++r) {
+        const float *row = c->w + r * c->k;
+        for (size_t i = 0; i < c->m; ++i) {
+            const float *x = c->x + i * c->k;
+            float acc = 0.0f;
+            for (size_t j = 0; j < c->k; ++j) {
+                float prod = row[j] * x[j];
+                acc = acc + prod;
+            }
+            c->y[i * c->n + r] = acc;
+        }
+    }
+}
+
+void kro_f32_matmul(const float *w, uint32_t n, uint32_t k, const float *x, uint32_t m, float *y, int nthreads) {
+    f32mm_ctx c = {w, n, k, m, x, y};
+    parallel_for(n, nthreads, f32mm_range, &c);
+}
+
 static float *bf16_rows_to_f32(const uint16_t *x, size_t count) {
     float *xf = (float *)malloc(sizeof(float) * (count ? count : 1));
     kro_bf16_to_f32_n(x, xf, count);

@@ -68,6 +68,10 @@ void kro_q4_matmul_f64(const uint32_t *qw, const uint16_t *sc, const uint16_t *b
                        uint32_t n, uint32_t k, const uint16_t *x_bf16, uint32_t m,
                        double *y, int nthreads);
 
+/* Sequential f32 dot of pre-dequantised rows w f32 [n, k] with x f32 [m, k] (the CPU
+ * baseline's upper bound: the reference test's dot without the per-call dequantisation). */
+void kro_f32_matmul(const float *w, uint32_t n, uint32_t k, const float *x, uint32_t m, float *y, int nthreads);
+
 /* ---- activation: q4_gemm_and_moe.metal:2064-2071, transformer_glue.metal:307-336 ---- */
 float kro_activation(float g, int variant); /* 0 SwiGLU(silu), 1 GeGLU(tanh), 2 ReLU */
 

@@ -142,3 +142,30 @@ def test_mlp_noalloc_rejects_sizes_beyond_its_scratch(kq):
     assert rc == kq.KR_E_WORKSPACE
     assert b"kr_q4_mlp_noalloc" in L.kr_last_error() and b"kr_q4_mlp with a workspace" in L.kr_last_error()
     assert L.kr_q4_mlp_workspace_bytes(37, 2048, 11008) <= 4 << 20 < L.kr_q4_mlp_workspace_bytes(38, 2048, 11008)
+
+
+def test_moe_block_argument_checks(kq):
+    """kr_q4_moe_block validates all three stages before its first launch (no GPU work here)."""
+    L = kq.lib()
+    E, H, I = 8, 256, 128
+    router = _mat(kq, n=E, k=H)
+    g, u = _mat(kq, n=E * I, k=H), _mat(kq, n=E * I, k=H)
+    d = _mat(kq, n=E * H, k=I)
+    x, y, ws = 0x40000, 0x50000, 0x60000
+    big = 1 << 30
+    args = lambda r=router, topk=2, act=0, dt=kq.DTYPE_F32: (ctypes.byref(r), ctypes.byref(g), ctypes.byref(u),  # noqa: E731
+                                                              ctypes.byref(d), E, x, 4, topk, 1, act, y, dt, 0, ws,
+                                                              big, None)
+    assert L.kr_q4_moe_block(*args(r=_mat(kq, n=E + 1, k=H))) == kq.KR_E_SHAPE
+    assert b"router" in L.kr_last_error()
+    assert L.kr_q4_moe_block(*args(topk=0)) == kq.KR_E_INVALID
+    assert L.kr_q4_moe_block(*args(topk=17)) == kq.KR_E_INVALID
+    assert L.kr_q4_moe_block(*args(act=9)) == kq.KR_E_INVALID
+    assert L.kr_q4_moe_block(*args(dt=7)) == kq.KR_E_INVALID
+    bad_down = _mat(kq, n=E * H, k=I + 64)
+    assert L.kr_q4_moe_block(ctypes.byref(router), ctypes.byref(g), ctypes.byref(u), ctypes.byref(bad_down), E, x, 4,
+                             2, 1, 0, y, kq.DTYPE_F32, 0, ws, big, None) == kq.KR_E_SHAPE
+    need = L.kr_q4_moe_block_workspace_bytes(4, E, 2, H, I)
+    assert need >= L.kr_q4_moe_workspace_bytes(4, 2, H, I)
+    assert L.kr_q4_moe_block(ctypes.byref(router), ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), E, x, 4, 2, 1,
+                             0, y, kq.DTYPE_F32, 0, ws, need - 1, None) == kq.KR_E_WORKSPACE

@@ -214,6 +214,38 @@ def test_moe_experts_with_an_unbucketed_assignment(kq):
         assert torch.isfinite(y).all()
 
 
+@pytest.mark.parametrize("T", [1, 64])
+def test_moe_block_router_to_combine(kq, T):
+    """Config 4 as one device stage (kr_q4_moe_block; encoder.rs:5246-5445): router Q4 GEMV with f32
+    logits -> routing -> experts -> combine, against the oracle's chain.  The block's first stage is
+    kr_q4_linear, whose logits are checked against the oracle's; the expected output routes on those
+    device logits, so that an expert whose probability ties within f32 rounding cannot flip the
+    comparison (both routings are compared too, and agree here)."""
+    E, K, H, I = 60, 4, 2048, 1408
+    case(f"moe block (router gemv -> route -> experts -> combine) T={T}")
+    s = synth()
+    router = s.q4_weight(E, H, 4801)
+    g, u = s.q4_weight(E * I, H, 4802), s.q4_weight(E * I, H, 4803)
+    d = s.q4_weight(E * H, I, 4804)
+    x = s.bf16_normal((T, H), 4805)
+    R, G, U, D = (q4_dev(kq, w) for w in (router, g, u, d))
+    xd = dev_bf16(x)
+    logits = kq.q4_linear(R, xd, out_dtype=kq.DTYPE_F32).cpu().numpy()
+    logits_cpu = O.q4_matmul(O.Q4Planar(*router), x)
+    assert_rms_close(logits, logits_cpu, what="router logits")
+    route = O.moe_route(logits, K, True)
+    route_cpu = O.moe_route(logits_cpu, K, True)
+    assert np.array_equal(route[0], route_cpu[0])
+    want = O.moe_experts(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), E, x, route[0], route[1])
+    y = kq.moe_block(R, G, U, D, E, xd, K).cpu().numpy()
+    assert_rms_close(y, want, what=f"moe block T={T}")
+    # accumulate into a bf16 residual (the layer's h += moe(x))
+    r0 = s.bf16_normal((T, H), 4806)
+    res = dev_bf16(r0).clone()
+    kq.moe_block(R, G, U, D, E, xd, K, y=res, accumulate=True)
+    assert_bf16_rounded_close(host_bits(res), O.bf16_to_f32(r0) + want, rms(want), rel=1e-2, what="moe block acc")
+
+
 def test_moe_crowded_experts(kq):
     """More than 16 tokens per expert: the 16-row chunk loop."""
     T, E, K, H, I = 40, 12, 2, 256, 128

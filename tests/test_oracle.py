@@ -323,3 +323,14 @@ def test_closed_form_fixtures_regress():
     # the reference test tolerance against its own f32 expectation (|gpu - cpu| < 0.05) holds trivially here
     w = O.Q4Planar(z["gemm_64x64x128_qw"], z["gemm_64x64x128_sc"], z["gemm_64x64x128_bi"])
     assert np.array_equal(O.q4_matmul(w, z["gemm_64x64x128_x"]), z["gemm_64x64x128_y"])
+
+
+def test_f32_matmul_on_predequantised_rows_equals_q4_matmul():
+    """The CPU baseline's upper-bound variant (dot on weights dequantised beforehand) performs the same
+    roundings in the same order as the faithful path, so the results are identical bit for bit."""
+    from kriya_q4 import synth
+    w = O.Q4Planar(*synth.q4_weight(97, 640, 61))
+    x = synth.bf16_normal((3, 640), 62)
+    a = O.q4_matmul(w, x, threads=3)
+    b = O.f32_matmul(O.dequant_planar(w), O.bf16_to_f32(x), threads=2)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
