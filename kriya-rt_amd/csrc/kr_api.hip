@@ -208,6 +208,14 @@ void choose_split_k(MfmaArgs &a, int bm, float *partial) {
 }
 
 }  // namespace
+
+// The message of kr_last_error() for the host-only parts of the library (csrc/safetensors.cpp).
+int set_error(int code, const char *msg) {
+    if (code == KR_OK) g_err.clear();
+    else g_err = msg;
+    return code;
+}
+
 }  // namespace kr
 
 using namespace kr;

@@ -18,7 +18,8 @@ crates/kriya-backend-metal/src/encoder.rs:4880-5484) for a dense Qwen2 layer:
 then logits = rmsnorm(h, ln_f) E^T with the tied Q4 embedding E (the LM head,
 encoder.rs:5506-5516) and the next token = argmax (greedy sampler).
 
-Weights are generated on the device (no checkpoint exists offline):
+Weights are generated on the device (no checkpoint exists offline), or read
+from a safetensors checkpoint with load_weights (kriya_q4.loader).  Generated:
 qw uniform u32, scales bf16(|N(0, 0.02)| + 1e-3), biases bf16(-8 scale), norm
 weights bf16(1 + 0.1 N), qkv biases bf16(0.1 N).  The KV cache of the first
 `ctx` positions is filled with bf16 N(0, 1).
@@ -145,6 +146,32 @@ class QwenQ4Decoder:
         self.next = torch.empty(batch, dtype=torch.int32, device=device)
         self.ws = rmsnorm_mlp_workspace(batch, c.hidden, c.inter, device=device)
         self.attn_ws = attention_workspace(batch, c.q_heads, c.head_dim, self.max_ctx, device=device)
+
+    def load_weights(self, archive) -> None:
+        """Replaces the random weights with a checkpoint's (a kriya_q4.loader.Archive in the Hugging Face /
+        MLX naming, validated first as validate_production_checkpoint does, encoder.rs:452-591); the KV
+        cache and token state are kept."""
+        c = self.cfg
+        kv = c.kv_heads * c.head_dim
+        qd = c.q_heads * c.head_dim
+        archive.validate_dense(c.hidden, c.inter, c.layers, c.vocab, c.q_heads, c.kv_heads, c.head_dim,
+                               qkv_bias=True, tie_word_embeddings=True)
+        self.embed = archive.load_q4("model.embed_tokens", c.vocab, c.hidden)
+        self.ln_f = archive.load_bf16("model.norm.weight", c.hidden)
+        for i, L in enumerate(self.layers):
+            p = f"model.layers.{i}"
+            L.ln1 = archive.load_bf16(f"{p}.input_layernorm.weight", c.hidden)
+            L.ln2 = archive.load_bf16(f"{p}.post_attention_layernorm.weight", c.hidden)
+            L.q = archive.load_q4(f"{p}.self_attn.q_proj", qd, c.hidden)
+            L.k = archive.load_q4(f"{p}.self_attn.k_proj", kv, c.hidden)
+            L.v = archive.load_q4(f"{p}.self_attn.v_proj", kv, c.hidden)
+            L.o = archive.load_q4(f"{p}.self_attn.o_proj", c.hidden, qd)
+            L.gate = archive.load_q4(f"{p}.mlp.gate_proj", c.inter, c.hidden)
+            L.up = archive.load_q4(f"{p}.mlp.up_proj", c.inter, c.hidden)
+            L.down = archive.load_q4(f"{p}.mlp.down_proj", c.hidden, c.inter)
+            L.bq = archive.load_bf16(f"{p}.self_attn.q_proj.bias", qd)
+            L.bk = archive.load_bf16(f"{p}.self_attn.k_proj.bias", kv)
+            L.bv = archive.load_bf16(f"{p}.self_attn.v_proj.bias", kv)
 
     def step(self, stream=None) -> torch.Tensor:
         """One greedy decode step at `positions`; returns the next-token buffer."""
