@@ -115,10 +115,22 @@ MfmaProblem problem(const Q4Mat &w, const Q4Mat *w2, void *out, const uint16_t *
 // is needed when the K split exceeds one block; without it the caller must use
 // another path (returns hipErrorInvalidValue).  `tickets` (kSkinnyTickets zero
 // words, left zero): the split is reduced inside the launch, else by a second one.
+// More than 16 rows (up to kSkinnyChunkMaxM): 16-row chunks, one launch each, in row order; each
+// reuses the partials and leaves the tickets at zero for the next.
 hipError_t run_skinny(const Q4Mat &w, const Q4Mat *w2, const uint16_t *x, uint32_t m, void *out,
                       const uint16_t *bias, uint32_t ldo, int out_dtype, int accumulate, int act, float *partial,
                       hipStream_t s, const uint16_t *ln_w = nullptr, float eps = 0.0f,
                       uint32_t *tickets = nullptr) {
+    if (m > kSkinnyMaxM) {
+        const size_t esz = dtype_size(out_dtype);
+        for (uint32_t i0 = 0; i0 < m; i0 += kSkinnyMaxM) {
+            const uint32_t mc = std::min(kSkinnyMaxM, m - i0);
+            if (hipError_t e = run_skinny(w, w2, x + (size_t)i0 * w.k, mc, (char *)out + (size_t)i0 * ldo * esz, bias, ldo,
+                                          out_dtype, accumulate, act, partial, s, ln_w, eps, tickets))
+                return e;
+        }
+        return hipSuccess;
+    }
     SkinnyArgs a{};
     a.ln_w = ln_w;
     a.eps = eps;
@@ -161,6 +173,17 @@ hipError_t run_skinny(const Q4Mat &w, const Q4Mat *w2, const uint16_t *x, uint32
 hipError_t run_skinny_qkv(const kr_q4_matrix *const *mats, const uint16_t *const *biases, void *const *outs,
                           const uint16_t *x, uint32_t m, int out_dtype, const uint16_t *ln_w, float eps,
                           hipStream_t s) {
+    if (m > kSkinnyMaxM) {  // 16-row chunks, as run_skinny
+        const size_t esz = dtype_size(out_dtype);
+        for (uint32_t i0 = 0; i0 < m; i0 += kSkinnyMaxM) {
+            void *o[3];
+            for (int i = 0; i < 3; ++i) o[i] = (char *)outs[i] + (size_t)i0 * mats[i]->n * esz;
+            if (hipError_t e = run_skinny_qkv(mats, biases, o, x + (size_t)i0 * mats[0]->k,
+                                              std::min(kSkinnyMaxM, m - i0), out_dtype, ln_w, eps, s))
+                return e;
+        }
+        return hipSuccess;
+    }
     SkinnyArgs a{};
     a.w = to_mat(mats[0]);
     a.x = x;
@@ -178,8 +201,11 @@ hipError_t run_skinny_qkv(const kr_q4_matrix *const *mats, const uint16_t *const
     return launch_skinny(a, s);
 }
 
+// The few-token kernel takes 2 <= m < 64 (above 16 rows in chunks): it is exact for any bf16 x,
+// where the reference keeps f32 tiles (q4_gemm_and_moe.metal:2173-2486); the prefill kernel stages
+// fp16, as the reference's M >= 64 kernels stage half.
 bool skinny_fits(uint32_t m, const Q4Mat &w, bool have_partial) {
-    return m >= 2 && m <= kSkinnyMaxM && skinny_supported(w) && (have_partial || skinny_ksplit(w.k) == 1);
+    return m >= 2 && m <= kSkinnyChunkMaxM && skinny_supported(w) && (have_partial || skinny_ksplit(w.k) == 1);
 }
 
 size_t partial_bytes(uint32_t m, uint32_t n, uint32_t k, int nw) {

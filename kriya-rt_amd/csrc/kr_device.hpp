@@ -135,6 +135,55 @@ __device__ __forceinline__ float wave_reduce_vec(typename FVec<N>::type v, int l
     return s;
 }
 
+// ---- activations outside fp16's range on the fp16 matrix-core paths.
+// fp16 holds a bf16 value exactly only within [2^-14, 65504]: a token row whose
+// largest |x| lies outside a safe window is staged times 2^e and its results
+// multiplied by 2^-e (both exact: powers of two).
+
+// Largest |value| of 8 bf16 values (a 16-byte unit) as non-negative bf16 bits:
+// magnitudes order as unsigned integers once the sign is cleared.
+__device__ __forceinline__ uint32_t bf16_unit_max_bits(const u32x4 &v) {
+    const uint32_t m = 0x7FFF7FFFu;
+    const auto pmax = [](uint32_t x, uint32_t y) -> uint32_t {  // per 16-bit half
+        return max(x & 0xFFFFu, y & 0xFFFFu) | (max(x >> 16, y >> 16) << 16);
+    };
+    const uint32_t p = pmax(pmax(v.x & m, v.y & m), pmax(v.z & m, v.w & m));
+    return max(p & 0xFFFFu, p >> 16);
+}
+
+// The exponent e for a row whose largest |x| has bf16 bits mb: 0 when its unbiased
+// exponent is within [lo, hi] (no scaling), else `target` - exponent, clamped so that
+// 2^e and 2^-e are normal floats.  Zero rows and rows holding inf or NaN get 0.
+__device__ __forceinline__ int row_stage_exp(uint32_t mb, int lo, int hi, int target) {
+    const int ef = (int)(mb >> 7);  // biased exponent field of a bf16
+    if (mb == 0u || ef == 0xFF) return 0;
+    const int ex = ef - 127;  // bf16 subnormals count as 2^-127
+    if (ex >= lo && ex <= hi) return 0;
+    return max(min(target - ex, 100), -100);
+}
+
+__device__ __forceinline__ float exp2_int(int e) { return __int_as_float((127 + e) << 23); }  // |e| <= 126
+
+// Unsigned max over aligned groups of 16 (or 8: HALF) lanes, left in every lane of the group:
+// DPP quad swaps, then the half-row (and row) mirror.
+template <bool HALF = false>
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false));  // half-row mirror
+    if (!HALF) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false));  // row mirror
+    return v;
+}
+
+// Unsigned max over the 64 lanes, as a wave-uniform value (row maxima, then the row broadcasts of
+// lanes 15 and 31; lane 63 ends with the maximum).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = row16_max_u32(v);
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x142, 0xA, 0xF, false));  // row bcast 15
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x143, 0xC, 0xF, false));  // row bcast 31
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int mask = 32; mask >= 1; mask >>= 1) v += __shfl_xor(v, mask);

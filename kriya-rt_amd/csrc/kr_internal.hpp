@@ -97,6 +97,7 @@ hipError_t launch_splitk_reduce(const MfmaArgs &a, int nw, hipStream_t s);
 
 // ---- few-token (m <= 16) and grouped MoE matrix-core path (q4_skinny.hip)
 constexpr uint32_t kSkinnyMaxM = 16;
+constexpr uint32_t kSkinnyChunkMaxM = 63;  // the host runs 17..63 rows as 16-row chunks
 constexpr uint32_t kMaxExperts = 256;
 struct SkinnyArgs {
     Q4Mat w, w2;            // w2: up matrix for the gate/up epilogue (qw == nullptr otherwise)

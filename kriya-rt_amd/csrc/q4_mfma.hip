@@ -17,7 +17,12 @@
 //     benchmark distributions; bf16 (8 bits) would round such weights.  The
 //     reference's own M >= 64 kernels use half operands as well
 //     (q4_gemm_and_moe.metal:2722-2724, 2761-2764).
-//   * activations: bf16 -> fp16 is exact for |x| in [2^-14, 65504].
+//   * activations: bf16 -> fp16 is exact for |x| in [2^-14, 65504].  A token row
+//     whose largest |x| over the block's K range lies outside [2^-8, 2^16) is
+//     staged times 2^e (its largest |x| then in [2^15, 2^16)) and its results
+//     multiplied by 2^-e, both exact; the row maxima come from a scan of the
+//     block's rows before the first step (this kernel serves the shapes the
+//     few-token and prefill kernels do not take).
 // Dequantisation per 8 nibbles (one u32 word): for j in 0..3 the pair of
 // nibbles (j, j+4) is placed under the fp16 pattern 0x6400 (1024.0, ulp 1),
 // v_pk_add_f16 removes the 1024 exactly and v_pk_fma_f16 applies (s, b).
@@ -50,12 +55,12 @@ __device__ __forceinline__ uint32_t opaque_v(uint32_t v) {
     return r;
 }
 
-// bf16 bits -> fp16 bits.  A bf16 value has 8 significant bits, so in fp16's
+// bf16 bits times 2^e (sc) -> fp16 bits.  A bf16 value has 8 significant bits, so in fp16's
 // normal range the conversion is exact and the rounding mode does not matter:
 // one v_cvt_pkrtz_f16_f32 per pair.
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v) {
-    return __builtin_bit_cast(uint32_t,
-                              __builtin_amdgcn_cvt_pkrtz(__uint_as_float(v << 16), __uint_as_float(v & 0xFFFF0000u)));
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v, float sc) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(__uint_as_float(v << 16) * sc,
+                                                                   __uint_as_float(v & 0xFFFF0000u) * sc));
 }
 
 // 8 nibbles of one word -> 8 fp16 weights in element order (e0..e7) as 4 u32.
@@ -101,6 +106,7 @@ template <int BM, int BN, int NW, int EPI>
 __global__ __launch_bounds__(256) void q4_mfma_gemm_kernel(MfmaArgs args) {
     using T = MfmaTile<BM, BN, NW>;
     extern __shared__ __align__(16) uint16_t lds_raw[];
+    __shared__ int s_rowexp[BM];  // staging exponent e of each token row of the block
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -169,11 +175,12 @@ __global__ __launch_bounds__(256) void q4_mfma_gemm_kernel(MfmaArgs args) {
             const uint32_t u = tid + 256 * i;
             if (u < (uint32_t)BM * 8) {
                 const uint32_t row = u >> 3, cb = u & 7;
+                const float sc = exp2_int(s_rowexp[row]);
                 u32x4 h;
-                h.x = bf16x2_to_f16x2(xr[i].x);
-                h.y = bf16x2_to_f16x2(xr[i].y);
-                h.z = bf16x2_to_f16x2(xr[i].z);
-                h.w = bf16x2_to_f16x2(xr[i].w);
+                h.x = bf16x2_to_f16x2(xr[i].x, sc);
+                h.y = bf16x2_to_f16x2(xr[i].y, sc);
+                h.z = bf16x2_to_f16x2(xr[i].z, sc);
+                h.w = bf16x2_to_f16x2(xr[i].w, sc);
                 *reinterpret_cast<u32x4 *>(base + row * kPitch + cb * 8) = h;
             }
         }
@@ -206,6 +213,20 @@ __global__ __launch_bounds__(256) void q4_mfma_gemm_kernel(MfmaArgs args) {
         for (int a = 0; a < T::kFragM; ++a)
 #pragma unroll
             for (int b = 0; b < T::kFragN; ++b) acc[mi][a][b] = f32x4{0, 0, 0, 0};
+
+    // ---- staging exponents of the block's token rows: wave w scans rows w, w + 4, ... over the
+    // block's K range (16-byte units strided by lane), maximum over the wave.
+    for (uint32_t r = (uint32_t)wave; r < (uint32_t)BM; r += 4) {
+        const uint32_t upr = (g_end > g_begin ? g_end - g_begin : 0u) * 8u;
+        uint32_t mx = 0;
+        if (m0 + r < args.m) {
+            const u32x4 *row = reinterpret_cast<const u32x4 *>(args.x + (size_t)(m0 + r) * args.ldx + g_begin * 64);
+            for (uint32_t c = (uint32_t)lane; c < upr; c += 64) mx = max(mx, bf16_unit_max_bits(row[c]));
+        }
+        mx = wave_max_u32(mx);
+        if (lane == 0) s_rowexp[r] = row_stage_exp(mx, -8, 15, 15);
+    }
+    __syncthreads();
 
     if (g_begin < g_end) {
         load_step(g_begin);
@@ -254,15 +275,17 @@ __global__ __launch_bounds__(256) void q4_mfma_gemm_kernel(MfmaArgs args) {
             for (int v = 0; v < 4; ++v) {
                 const uint32_t m = m0 + wm * T::kWaveM + a * 16 + 4 * (lane >> 4) + v;
                 if (m >= args.m) continue;
+                const float unscale = exp2_int(-s_rowexp[m - m0]);  // the row's staging scale undone
+                const float g0 = acc[0][a][b][v] * unscale, u0 = acc[NW - 1][a][b][v] * unscale;
                 if (EPI == kMfmaPartial) {
                     // split-K partials: [split][m][NW * N]
                     float *dst = args.partial + ((size_t)ks * args.m + m) * (size_t)(NW * N) + n;
-                    dst[0] = acc[0][a][b][v];
-                    if (NW == 2) dst[N] = acc[NW - 1][a][b][v];
+                    dst[0] = g0;
+                    if (NW == 2) dst[N] = u0;
                     continue;
                 }
-                float val = acc[0][a][b][v];
-                if (NW == 2) val = activation(val, args.act) * acc[NW - 1][a][b][v];
+                float val = g0;
+                if (NW == 2) val = activation(val, args.act) * u0;
                 if (P.bias) val += bf16_to_f32(P.bias[n]);
                 const size_t o = (size_t)m * P.ldo + n;
                 if (args.out_f32) {

@@ -10,7 +10,13 @@
 // v_mfma_f32_16x16x32_f16.  Operand numerics are those of the reference's M >= 64
 // kernels (half operands, q4_gemm_and_moe.metal:2722-2724, 2761-2764):
 //   * w = fma(q, s, b) rounded once to fp16 (s, b: bf16 -> fp16 RNE);
-//   * x: bf16 -> fp16 RNE, exact for |x| in [2^-14, 65504].
+//   * x: bf16 -> fp16 RNE, exact for |x| in [2^-14, 65504]; smaller values become
+//     fp16 subnormals (the reference's M >= 64 kernels stage half as well).  A value
+//     beyond 65504 turns into inf, and so does its block's result: a block whose
+//     accumulators come out non-finite computes its tile again in plain f32
+//     arithmetic (dequantised weights times bf16 x, exact products of the inputs'
+//     values), which writes the outputs itself.  Ordinary data never takes that
+//     path.  The few-token kernel, exact in bf16, serves m < 64 (q4_skinny.hip).
 //
 // Where the time goes at these shapes (M = 512, K = 2048 .. 11008): dequantising
 // a nibble costs ~2 VALU lane-ops, converting an X element ~1.5, and the matrix
@@ -204,6 +210,19 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
             *p = x_unit_f16(*p);
         }
     };
+    // Block-wide OR without LDS of its own (a static LDS array would cost the 64-row shape one of
+    // its five blocks per CU): each wave's ballot goes to a flag byte in X buffer 0, a barrier, then
+    // every lane reads the WAVES flags.  Only after the last step, when no load writes the buffers.
+    auto block_any = [&](bool pred) -> bool {
+        int8_t *flags = reinterpret_cast<int8_t *>(lds);
+        const bool wave_any = __ballot(pred) != 0ull;
+        if (lane == 0) flags[wave] = wave_any ? 1 : 0;
+        __syncthreads();
+        bool any = false;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) any |= flags[w] != 0;
+        return any;
+    };
     // A fragment of slice j: row r = 16 * a + c (the swizzle depends on c only), unit
     // 2 kq + j (SW = 1) or 4 kq + j (SW = 2): the lane's 8 columns of that slice
     uint32_t xa[kSlices];
@@ -320,6 +339,63 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
             if (g + 2 < g_end) step(S2{}, g + 2);
         }
     }
+    // Exact fallback (see the top of the file): a non-finite accumulator sends the block to a plain f32
+    // computation of its tile (rows beyond M and columns beyond N skipped), which writes the outputs.
+    bool bad = false;
+#pragma unroll
+    for (int a = 0; a < MF; ++a)
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) bad |= !__builtin_isfinite(acc[a][f][v]);
+    if (block_any(bad)) {
+        const uint32_t c0 = g_begin * 64 * SW, c1 = min(g_end * SW, G) * 64;
+        const uint32_t outs = T::kBM * T::kBN;
+        for (uint32_t o = (uint32_t)tid; o < outs; o += 64 * WAVES) {
+            const uint32_t mi = o / T::kBN, ni = o % T::kBN;
+            const uint32_t m = m0 + mi;
+            const uint32_t fw = ni / T::kWaveRows, fr = ni % T::kWaveRows;  // wave, row of its fragments
+            const uint32_t n = nt * T::kBN + fw * T::kWaveRows + fr;
+            if (m >= M || n >= N) continue;
+            float gsum = 0.0f, usum = 0.0f;
+            const uint16_t *xr = args.x + (size_t)m * args.ldx;
+            for (uint32_t c = c0; c < c1; c += 8) {
+                const uint32_t wq = P.w.qw[(size_t)n * (K >> 3) + (c >> 3)];
+                const float sc = bf16_to_f32(P.w.sc[(size_t)n * G + (c >> 6)]), bi = bf16_to_f32(P.w.bi[(size_t)n * G + (c >> 6)]);
+                uint32_t uq = 0;
+                float usc = 0.0f, ubi = 0.0f;
+                if (NW == 2) {
+                    uq = P.w2.qw[(size_t)n * (K >> 3) + (c >> 3)];
+                    usc = bf16_to_f32(P.w2.sc[(size_t)n * G + (c >> 6)]);
+                    ubi = bf16_to_f32(P.w2.bi[(size_t)n * G + (c >> 6)]);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float x = bf16_to_f32(xr[c + j]);
+                    gsum = fmaf(fmaf((float)((wq >> (4 * j)) & 15u), sc, bi), x, gsum);
+                    if (NW == 2) usum = fmaf(fmaf((float)((uq >> (4 * j)) & 15u), usc, ubi), x, usum);
+                }
+            }
+            if (EPI == kMfmaPartial) {
+                float *dst = args.partial + ((size_t)ks * M + m) * (size_t)(NW * N) + n;
+                dst[0] = gsum;
+                if (NW == 2) dst[N] = usum;
+                continue;
+            }
+            float val = gsum;
+            if (NW == 2) val = activation(val, args.act) * usum;
+            if (EPI == kMfmaDirect && P.bias) val += bf16_to_f32(P.bias[n]);
+            const size_t oo = (size_t)m * P.ldo + n;
+            if (args.out_f32) {
+                float *out = reinterpret_cast<float *>(P.out);
+                out[oo] = args.accumulate ? out[oo] + val : val;
+            } else {
+                uint16_t *out = reinterpret_cast<uint16_t *>(P.out);
+                out[oo] = (uint16_t)f32_to_bf16(args.accumulate ? val + bf16_to_f32(out[oo]) : val);
+            }
+        }
+        return;
+    }
 
     // ---- epilogue: lane holds C[4 * kq + v][c] of each 16 x 16 fragment
 #pragma unroll
@@ -333,14 +409,16 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
             for (int v = 0; v < 4; ++v) {
                 const uint32_t m = m0 + a * 16 + 4 * kq + v;
                 if (m >= M) continue;
+                const float g0 = acc[a][fo][v];
+                const float u0 = NW == 2 ? acc[a][fo + FPM][v] : 0.0f;
                 if (EPI == kMfmaPartial) {
                     float *dst = args.partial + ((size_t)ks * M + m) * (size_t)(NW * N) + n;
-                    dst[0] = acc[a][fo][v];
-                    if (NW == 2) dst[N] = acc[a][fo + FPM][v];
+                    dst[0] = g0;
+                    if (NW == 2) dst[N] = u0;
                     continue;
                 }
-                float val = acc[a][fo][v];
-                if (NW == 2) val = activation(val, args.act) * acc[a][fo + FPM][v];
+                float val = g0;
+                if (NW == 2) val = activation(val, args.act) * u0;
                 val += bias;
                 const size_t o = (size_t)m * P.ldo + n;
                 if (args.out_f32) {

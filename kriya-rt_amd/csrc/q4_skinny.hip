@@ -8,27 +8,36 @@
 //
 // Bound: HBM (each weight is read once per launch; 16 tokens give AI <= 57 FLOP/B).
 //
-// Mapping.  v_mfma_f32_16x16x32_f16 with A = X (16 token rows, zero-padded)
-// and B = W^T (16 weight rows).  A block takes a tile of 16 weight rows over a
-// K slab of 2048 columns; wave w multiplies the slab's 128-column pieces
-// 2w, 2w + 1 and the 8 waves' 16 x 16 partial tiles are summed through LDS in
-// wave order (fixed order: results do not depend on timing).  The next tile's
-// words are requested before the current tile is multiplied (two register
-// buffers), and the epilogue's operands (bias, old output) with them, so that
-// no wait on them also waits for the prefetch in flight.  Barriers are
-// LDS-only (s_barrier after an lgkmcnt wait): a fenced barrier would wait for
-// the prefetch.
+// Mapping.  v_mfma_f32_16x16x32_bf16 with A = X (16 token rows, zero-padded)
+// and B = the exact integers 128 + q (16 weight rows); the affine map of each
+// 64-column group is applied to the f32 results, as the GEMV does:
+//   sum_c x_c (s q_c + b) = s * D + (b - 128 s) * S,  D = sum_c x_c (128 + q_c),  S = sum_c x_c
+// (the reference's distributive block dot, q4_gemm_and_moe.metal:414-473).  Both
+// products are exact in bf16 (bf16 x, integers below 256) and sum in f32, so x
+// keeps its full bf16 range: there is no fp16 conversion of x or of w.  S comes
+// from the same X fragments times a fragment of ones on the matrix cores.
+// A block takes a tile of 16 weight rows over a K slab of 2048 columns; wave w
+// multiplies the slab's 128-column pieces 2w, 2w + 1 and the 8 waves' 16 x 16
+// partial tiles are summed through LDS in wave order (fixed order: results do
+// not depend on timing).  The next tile's words are requested before the
+// current tile is multiplied (two register buffers), and the epilogue's
+// operands (bias, old output) with them, so that no wait on them also waits for
+// the prefetch in flight.  Barriers are LDS-only (s_barrier after an lgkmcnt
+// wait): a fenced barrier would wait for the prefetch.
 // Loads: lane (r16, g) reads 16 bytes of piece p of row r16 (columns 128 p +
 // 32 g .. + 31), so one wave instruction reads 64 contiguous bytes of each of
-// 16 rows.  Word j of those 16 bytes is that lane's k-block of MFMA slice
-// (p, j).  The matching X fragment comes from LDS, where the block staged the
-// slab's X rows once as fp16 in the order e0 e4 e1 e5 e2 e6 e3 e7 of every 8
-// columns (the order the nibble pairs unpack in), in 16-byte units
-// XOR-swizzled by row so that the 16 rows of a read hit distinct banks.
+// 16 rows: lanes 0-31 hold group 2p, lanes 32-63 group 2p + 1.  Words 2q and
+// 2q + 1 are swapped across the lane halves (v_permlane32_swap), after which
+// one register holds group 2p in every lane and the other group 2p + 1: each
+// matrix instruction contracts within one group.  The matching X fragments
+// come from LDS, where the block staged the slab's X rows once, bf16, in the
+// order e0 e4 e1 e5 e2 e6 e3 e7 of every 8 columns (the order the nibble pairs
+// unpack in), in 16-byte units XOR-swizzled by row so that the 16 rows of a read
+// hit distinct banks.
 // Scales and biases: every lane loads the bf16 pair (groups 2p, 2p + 1) of its
-// row and piece and takes the half of its lane group.
-// Dequantisation in registers: nibble pairs (j, j+4) under the fp16 pattern
-// 0x6400 -> exact (1024+q) halves, v_pk_add_f16 -1024, v_pk_fma_f16 (s, b).
+// row and piece; the results of lane (r16, .) belong to weight row r16.
+// Unpacking: nibble pairs (j, j + 4) of a word under the bf16 pattern 0x4300
+// -> the exact values (128 + q_j, 128 + q_{j+4}), one v_and_or_b32 each.
 // Gate/up: a tile holds 8 gate rows (lanes 0-7) and the same 8 up rows (lanes
 // 8-15); the epilogue pairs column c with column c + 8.
 // K longer than one slab is split over blocks (one slab each) and the f32
@@ -64,40 +73,17 @@ __device__ __forceinline__ uint32_t opq_v(uint32_t v) {
     return r;
 }
 
-// 8 bf16 x values (4 u32 words, element order) -> 8 fp16 in the order e0 e4 e1 e5 e2 e6 e3 e7.
+// 8 bf16 x values (4 u32 words, element order) -> the same 8 bf16 in the order e0 e4 e1 e5 e2 e6 e3 e7.
 __device__ __forceinline__ u32x4 x_unit(const u32x4 &v) {
-    const uint32_t X[4] = {v.x, v.y, v.z, v.w};
-    _Float16 e[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        e[2 * i] = (_Float16)__uint_as_float(X[i] << 16);
-        e[2 * i + 1] = (_Float16)__uint_as_float(X[i] & 0xFFFF0000u);
-    }
-    const f16x8_t r = {e[0], e[4], e[1], e[5], e[2], e[6], e[3], e[7]};
-    return __builtin_bit_cast(u32x4, r);
+    return u32x4{__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                 __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u)};
 }
 
-// one word of 8 nibbles -> B fragment (w0 w4 w1 w5 w2 w6 w3 w7) as fp16
-__device__ __forceinline__ f16x8_t w_frag(uint32_t w, f16x2_t s2, f16x2_t b2, uint32_t mask, uint32_t magic) {
-    const f16x2_t k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
-    f16x2_t pr[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const f16x2_t q = __builtin_bit_cast(f16x2_t, ((w >> (4 * j)) & mask) | magic) + k1024;
-        pr[j] = __builtin_elementwise_fma(q, s2, b2);
-    }
-    f16x8_t r = {pr[0].x, pr[0].y, pr[1].x, pr[1].y, pr[2].x, pr[2].y, pr[3].x, pr[3].y};
-    return r;
-}
-
-// (bf16 lo, bf16 hi) -> (fp16 lo, fp16 hi), round to nearest even
-__device__ __forceinline__ uint32_t f16_pair_of_bf16_pair(uint32_t p) {
-    const f16x2_t h = {(_Float16)__uint_as_float(p << 16), (_Float16)__uint_as_float(p & 0xFFFF0000u)};
-    return __builtin_bit_cast(uint32_t, h);
-}
-
-__device__ __forceinline__ uint32_t word_of(const u32x4 &v, int i) {
-    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+// one word of 8 nibbles -> B fragment (128 + q) in the order (w0 w4 w1 w5 w2 w6 w3 w7), bf16
+__device__ __forceinline__ bf16x8_t q_frag(uint32_t w, uint32_t mask, uint32_t magic) {
+    const u32x4 r = {(w & mask) | magic, ((w >> 4) & mask) | magic, ((w >> 8) & mask) | magic,
+                     ((w >> 12) & mask) | magic};
+    return __builtin_bit_cast(bf16x8_t, r);
 }
 
 // LDS position of 16-byte X unit u (8 columns) of row r (XOR swizzle by row).
@@ -122,7 +108,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     constexpr uint32_t kTileRows = kGateUp ? 8 : 16;  // output features per tile
     constexpr int kUnits = NW * KW * 16;               // 16-byte X units per LDS row
     constexpr int kStage = 16 * kUnits / (NW * 64);    // X units staged per thread
-    __shared__ u32x4 xs[16 * kUnits];                  // X slab: 16 rows x kSlabCols fp16
+    __shared__ u32x4 xs[16 * kUnits];                  // X slab: 16 rows x kSlabCols bf16
     __shared__ float red[2][NW][4][64];                // per-wave partial tiles, double buffered
 
     const int tid = threadIdx.x;
@@ -135,7 +121,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     const uint32_t npieces = min((uint32_t)(NW * KW), (K - k0) >> 7);  // live pieces of the slab (K % 128 == 0)
     const uint32_t p0 = (uint32_t)wave * KW;                           // this wave's first piece
     const uint32_t kMask = opq_s(0x000F000Fu);
-    const uint32_t kMagic = opq_v(0x64006400u);
+    const uint32_t kMagic = opq_v(0x43004300u);  // bf16 128.0 in both halves
 
     // ---- active experts (grouped mode), held in registers: lane l covers experts l + 64 i
     constexpr int kEPer = kGrouped ? (int)(kMaxExperts / 64) : 1;
@@ -353,51 +339,56 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         }
     };
 
-    // X fragment of slice (i, j) of this wave: unit 16 (p0 + i) + 4 g + j of row
-    // r16, i.e. (swizzle) r16 * kUnits + 16 (p0 + i) + ((4 g + j) ^ r16): one
-    // base per j, and i as an immediate offset.  The low 32 bits of a generic
-    // LDS pointer are its LDS offset.
-    uint32_t xaddr[4];
+    // X fragments of piece i for its four matrix instructions (h = group 2p + h, q = words 2q, 2q + 1):
+    // lane group g reads unit 16 (p0 + i) + 4 (g & 1) + (g >> 1) + 2 q + 8 h of row r16, i.e.
+    // (swizzle) r16 * kUnits + 16 (p0 + i) + (unit ^ r16): one base per (h, q), and i as an immediate
+    // offset.  The low 32 bits of a generic LDS pointer are its LDS offset.
+    uint32_t xaddr[4];  // [2 h + q]
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        xaddr[j] = (uint32_t)reinterpret_cast<uintptr_t>(
-            &xs[(uint32_t)r16 * kUnits + 16u * p0 + ((4u * (uint32_t)g + (uint32_t)j) ^ (uint32_t)r16)]);
-    // The four X fragments of piece i in one batch: four reads in flight, one wait.
-    auto xread4 = [&](int i, f16x8_t (&x)[4]) {
-        u32x4 v0, v1, v2, v3;
+    for (uint32_t hq = 0; hq < 4; ++hq) {
+        const uint32_t unit = 4u * ((uint32_t)g & 1u) + ((uint32_t)g >> 1) + 2u * (hq & 1u) + 8u * (hq >> 1);
+        xaddr[hq] = (uint32_t)reinterpret_cast<uintptr_t>(&xs[(uint32_t)r16 * kUnits + 16u * p0 + (unit ^ (uint32_t)r16)]);
+    }
+    // The two X fragments of group 2p + h of piece i: two reads in flight, one wait.
+    auto xread2 = [&](int i, int h, bf16x8_t (&x)[2]) {
+        u32x4 v0, v1;
         asm volatile(
-            "ds_read_b128 %0, %4 offset:%8\n\t"
-            "ds_read_b128 %1, %5 offset:%8\n\t"
-            "ds_read_b128 %2, %6 offset:%8\n\t"
-            "ds_read_b128 %3, %7 offset:%8\n\t"
+            "ds_read_b128 %0, %2 offset:%4\n\t"
+            "ds_read_b128 %1, %3 offset:%4\n\t"
             "s_waitcnt lgkmcnt(0)"
-            : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3)
-            : "v"(xaddr[0]), "v"(xaddr[1]), "v"(xaddr[2]), "v"(xaddr[3]), "i"(256 * i)
+            : "=&v"(v0), "=&v"(v1)
+            : "v"(xaddr[2 * h]), "v"(xaddr[2 * h + 1]), "i"(256 * i)
             : "memory");
-        x[0] = __builtin_bit_cast(f16x8_t, v0);
-        x[1] = __builtin_bit_cast(f16x8_t, v1);
-        x[2] = __builtin_bit_cast(f16x8_t, v2);
-        x[3] = __builtin_bit_cast(f16x8_t, v3);
+        x[0] = __builtin_bit_cast(bf16x8_t, v0);
+        x[1] = __builtin_bit_cast(bf16x8_t, v1);
     };
 
-    // v_perm selector broadcasting this lane's half (group 2p + g/2) of a pair to both halves
-    const uint32_t half_sel = (g >> 1) ? 0x03020302u : 0x01000100u;
+    const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
     auto tile_mma = [&](auto BUF) -> f32x4 {
         constexpr int b = decltype(BUF)::value;
         f32x4 acc = {0, 0, 0, 0};
+        const f32x4 zero = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < KW; ++i) {
+            // past the slab: the re-read words meet zero X; zero scales keep the products at 0
             const bool live = p0 + (uint32_t)i < npieces;
-            const uint32_t sh = live ? f16_pair_of_bf16_pair(sp[b][i]) : 0u;
-            const uint32_t bh = live ? f16_pair_of_bf16_pair(bp[b][i]) : 0u;
-            const f16x2_t s2 = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0u, sh, half_sel));
-            const f16x2_t b2 = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0u, bh, half_sel));
-            f16x8_t xp[4];
-            xread4(i, xp);
+            const uint32_t sv = live ? sp[b][i] : 0u, bv = live ? bp[b][i] : 0u;
+            // swap words (0, 1) and (2, 3) across the lane halves: [0] holds group 2p, [1] group 2p + 1
+            const auto p01 = __builtin_amdgcn_permlane32_swap(wv[b][i].x, wv[b][i].y, false, false);
+            const auto p23 = __builtin_amdgcn_permlane32_swap(wv[b][i].z, wv[b][i].w, false, false);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xp[j], w_frag(word_of(wv[b][i], j), s2, b2, kMask, kMagic),
-                                                             acc, 0, 0, 0);
+            for (int h = 0; h < 2; ++h) {  // one group at a time: fewer registers live
+                const float sg = __uint_as_float(h ? (sv & 0xFFFF0000u) : (sv << 16));
+                const float cg = fmaf(-128.0f, sg, __uint_as_float(h ? (bv & 0xFFFF0000u) : (bv << 16)));
+                bf16x8_t xp[2];
+                xread2(i, h, xp);
+                f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[0], q_frag(p01[h], kMask, kMagic), zero, 0, 0, 0);
+                f32x4 sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[0], ones, zero, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[1], q_frag(p23[h], kMask, kMagic), d, 0, 0, 0);
+                sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[1], ones, sx, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[v] = fmaf(cg, sx[v], fmaf(sg, d[v], acc[v]));
+            }
         }
         return acc;
     };
