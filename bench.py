@@ -8,6 +8,7 @@ copies totalling > 1 GB so that the 256 MB MALL cannot serve them; the step
 sequence is captured once in a HIP graph and replayed.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+       python bench.py --profile prefill|few|gemv   (short eager run for rocprofv3 counter passes)
 """
 from __future__ import annotations
 
@@ -350,6 +351,57 @@ def copy_calibration(torch):
     log("copied 4 x 256 MiB")
 
 
+def profile_run(kq, torch, synth, what, reps=8):
+    """Short eager runs for rocprofv3 counter passes (--profile): each workload's launches `reps` times on two
+    weight copies (few dispatches, so every counter pass stays short).
+      prefill: cfg2's layer at M = 512 (q/k/v in one launch, o accumulated, gate/up + SwiGLU, split-K down);
+      few:     cfg1's MLP at B = 16 (few-token gate/up, down with the in-launch split-K reduction) and cfg4's
+               grouped experts at T = 64;
+      gemv:    cfg1's MLP at B = 1 (the headline kernels)."""
+    H, I, KV = synth.HIDDEN, synth.INTER, 256
+    if what == "prefill":
+        M = 512
+        shapes = [(H, H), (KV, H), (KV, H), (H, H), (I, H), (I, H), (H, I)]
+        rot = Rotation(kq, torch, [synth.q4_weight(n, k, 2000 + i) for i, (n, k) in enumerate(shapes)], 2)
+        x = torch.from_numpy(synth.bf16_normal((M, H), 2100).view(np.int16)).cuda().view(torch.bfloat16)
+        qo = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+        ko = torch.empty((M, KV), dtype=torch.bfloat16, device="cuda")
+        vo = torch.empty_like(ko)
+        h = x.clone()
+        ws = kq.mlp_workspace(M, H, I)
+        for i in range(reps):
+            q, k, v, o, g, u, d = rot.sets[i % 2]
+            kq.qkv(q, k, v, x, out_dtype=kq.DTYPE_BF16, outs=(qo, ko, vo))
+            kq.q4_linear(o, x, y=h, accumulate=True)
+            kq.mlp(g, u, d, h, x=x, workspace=ws)
+    elif what in ("few", "gemv"):
+        B = 16 if what == "few" else 1
+        rot = Rotation(kq, torch, [synth.q4_weight(I, H, 1001), synth.q4_weight(I, H, 1002),
+                                   synth.q4_weight(H, I, 1003)], 2)
+        h = torch.from_numpy(synth.bf16_normal((B, H), 1010 + B).view(np.int16)).cuda().view(torch.bfloat16)
+        xs = h.clone()
+        ws = kq.mlp_workspace(B, H, I)
+        for i in range(reps):
+            g, u, d = rot.sets[i % 2]
+            kq.mlp(g, u, d, h, x=xs, workspace=ws)
+        if what == "few":
+            E, K, T, Im = 60, 4, 64, 1408
+            mrot = Rotation(kq, torch, [synth.q4_weight(E * Im, H, 4001), synth.q4_weight(E * Im, H, 4002),
+                                        synth.q4_weight(E * H, Im, 4003)], 2)
+            x = torch.from_numpy(synth.bf16_normal((T, H), 4004).view(np.int16)).cuda().view(torch.bfloat16)
+            logits = torch.from_numpy(synth.f32_normal((T, E), 4005)).cuda()
+            r = kq.moe_route(logits, K, True)
+            y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+            mws = kq.moe_workspace(T, K, H, Im)
+            for i in range(reps):
+                g, u, d = mrot.sets[i % 2]
+                kq.moe_experts(g, u, d, E, x, r, y=y, workspace=mws)
+    else:
+        raise SystemExit(f"--profile: unknown workload {what!r} (prefill, few, gemv)")
+    torch.cuda.synchronize()
+    log(f"profile run '{what}' done ({reps} repetitions)")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -360,6 +412,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a 4 x 256 MiB device copy (PMC byte-counter calibration)")
+    ap.add_argument("--profile", choices=["prefill", "few", "gemv"],
+                    help="only a short eager run of one workload, for rocprofv3 counter passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported in this build "
@@ -376,6 +430,9 @@ def main():
         copy_calibration(torch)
         return
     kq.lib()
+    if args.profile:
+        profile_run(kq, torch, synth, args.profile)
+        return
     log(f"device {torch.cuda.get_device_name(0)}")
 
     log("cfg1 B=1 (headline)")

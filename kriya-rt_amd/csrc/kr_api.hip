@@ -71,17 +71,6 @@ size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 constexpr uint32_t kMaxSplitK = 8;
 
-int device_cus() {
-    static thread_local int dev = -1, cus = 0;
-    int d = 0;
-    if (hipGetDevice(&d) != hipSuccess) d = 0;
-    if (d != dev) {
-        dev = d;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || cus <= 0) cus = 256;
-    }
-    return cus;
-}
-
 // M tile class of the matrix-core kernels: 32-row tiles for batched decode,
 // 64 or 128 rows for prefill.
 int bm_class(uint32_t m) { return m <= 16 ? 16 : (m <= 64 ? 64 : 128); }
@@ -234,6 +223,17 @@ void choose_split_k(MfmaArgs &a, int bm, float *partial) {
 }
 
 }  // namespace
+
+int device_cus() {
+    static thread_local int dev = -1, cus = 0;
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess) d = 0;
+    if (d != dev) {
+        dev = d;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || cus <= 0) cus = 256;
+    }
+    return cus;
+}
 
 // The message of kr_last_error() for the host-only parts of the library (csrc/safetensors.cpp).
 int set_error(int code, const char *msg) {

@@ -90,6 +90,7 @@ hipError_t launch_mfma(MfmaArgs &a, int bm, hipStream_t s);
 // Prefill kernel (q4_prefill.hip): m > 16, k % 64 == 0, operands < 4 GiB.
 bool prefill_supported(const MfmaArgs &a);
 hipError_t launch_prefill(MfmaArgs &a, hipStream_t s);
+int device_cus();                               // compute units of the current device
 uint32_t prefill_block_m(bool gate_up);         // token rows per block
 uint32_t prefill_block_rows(bool gate_up);      // weight rows (per matrix) per block
 // Fixed-order sum of split-K partials [ksplit, m, nw * N] + the epilogue of p[0].

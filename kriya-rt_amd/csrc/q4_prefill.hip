@@ -38,6 +38,12 @@
 //   * weights, scales and X are read through buffer resources with the block-
 //     and step-uniform part of every offset in an SGPR; every offset is kept in
 //     range on the host side of the check (tail rows are clamped, never stored).
+//   * the A fragments of the next 32-column slice are read from LDS before the
+//     current slice's dequantisation and matrix instructions;
+//   * the epilogue stages the block's tile in LDS, so each thread stores 8
+//     consecutive columns of a row (16-byte stores) instead of 2- or 4-byte pieces;
+//   * shapes with fewer tiles than two per CU run two groups of waves per tile
+//     that split its steps and add their accumulators through LDS.
 // Gate/up: a wave's fragments are FPM gate fragments followed by FPM up
 // fragments of the same rows, so act(g) * u is formed lane-locally.
 // Block ids are remapped so that the M tiles of one N tile run on one XCD and
@@ -107,10 +113,10 @@ __device__ __forceinline__ u32x4 x_unit_f16(u32x4 d) {
 
 }  // namespace
 
-template <int MF, int NF, int WAVES, int NW>
+template <int MF, int NF, int WAVES, int NW, int KW = 1>
 struct PrefillTile {
     static constexpr int kBM = MF * 16;                 // token rows per block
-    static constexpr int kThreads = 64 * WAVES;
+    static constexpr int kThreads = 64 * WAVES * KW;
     static constexpr int kFPM = NF / NW;                // fragments per matrix per wave
     static constexpr int kWaveRows = kFPM * 16;         // output columns per wave
     static constexpr int kBN = WAVES * kWaveRows;       // output columns per block
@@ -127,9 +133,14 @@ struct PrefillTile {
 // weights of a step are one 16-byte load (32 nibbles: four MFMA slices) and
 // its scales and biases one 4-byte pair each: half the load instructions of
 // SW = 1, whose lanes load 8 bytes and two 2-byte values per 64 columns.
-template <int MF, int NF, int WAVES, int NW, int OCC, int EPI, int D, int SW>
-__global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs args) {
-    using T = PrefillTile<MF, NF, WAVES, NW>;
+// KW: groups of WAVES waves that split the block's steps (group k takes steps
+// k, k + KW, ...; each group has its own X ring) and add their accumulators
+// through LDS in group order at the end.  Shapes with few tiles (N = 2048)
+// get KW waves per tile instead of one: more waves per SIMD to overlap the
+// latencies of each wave's step, with no workspace.
+template <int MF, int NF, int WAVES, int NW, int OCC, int EPI, int D, int SW, int KW>
+__global__ __launch_bounds__(64 * WAVES * KW, OCC) void q4_prefill_kernel(MfmaArgs args) {
+    using T = PrefillTile<MF, NF, WAVES, NW, KW>;
     constexpr int FPM = T::kFPM;
     constexpr int kUnits = 8 * SW;                  // 16-byte X units per LDS row
     constexpr int kBuf = T::kBM * 16 * kUnits;      // bytes of one X slice
@@ -138,8 +149,10 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
     extern __shared__ __align__(16) char lds[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wave = wid % WAVES, kg = wid / WAVES;  // wave within its K group, the group
     const int c = lane & 15, kq = lane >> 4;
+    char *const xring = lds + kg * (D + 1) * kBuf;  // this group's X buffers
 
     // ---- block -> (problem, n tile, m tile); the M tiles of one N tile share an XCD
     const uint32_t nblk = gridDim.x;
@@ -188,7 +201,7 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
     // wave writes 64 consecutive slots (lane l -> slot base + l), so each lane
     // loads the global unit that belongs in its slot and later converts exactly
     // the slots it loaded (its own data: no barrier between load and convert).
-    auto swizzle = [](uint32_t r) -> uint32_t { return SW == 1 ? swz(r) : (r & 15); };
+    auto swizzle = [](uint32_t r) -> uint32_t { return SW == 1 ? swz(r) : (((r & 7) << 1) | ((r >> 3) & 1)); };
     constexpr int XI = T::kBM * kUnits / 64 / WAVES;  // DMA instructions per wave per step
     static_assert(T::kBM * kUnits % (64 * WAVES) == 0, "X slice must split into whole DMA instructions");
     const rsrc_t rx = make_rsrc(args.x, (M - 1) * args.ldx * 2 + K * 2);
@@ -201,12 +214,12 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
     }
     auto dma_x = [&](uint32_t g, int buf) {
 #pragma unroll
-        for (int i = 0; i < XI; ++i) dma16(rx, lds + buf * kBuf + (wave * XI + i) * 1024, xo[i], g * (128 * SW));
+        for (int i = 0; i < XI; ++i) dma16(rx, xring + buf * kBuf + (wave * XI + i) * 1024, xo[i], g * (128 * SW));
     };
     auto convert_x = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < XI; ++i) {
-            u32x4 *p = reinterpret_cast<u32x4 *>(lds + buf * kBuf + (wave * XI + i) * 1024 + lane * 16);
+            u32x4 *p = reinterpret_cast<u32x4 *>(xring + buf * kBuf + (wave * XI + i) * 1024 + lane * 16);
             *p = x_unit_f16(*p);
         }
     };
@@ -216,11 +229,11 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
     auto block_any = [&](bool pred) -> bool {
         int8_t *flags = reinterpret_cast<int8_t *>(lds);
         const bool wave_any = __ballot(pred) != 0ull;
-        if (lane == 0) flags[wave] = wave_any ? 1 : 0;
+        if (lane == 0) flags[wid] = wave_any ? 1 : 0;
         __syncthreads();
         bool any = false;
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) any |= flags[w] != 0;
+        for (int w = 0; w < WAVES * KW; ++w) any |= flags[w] != 0;
         return any;
     };
     // A fragment of slice j: row r = 16 * a + c (the swizzle depends on c only), unit
@@ -272,19 +285,47 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
             s2[f] = f16_pair(sb);
             b2[f] = f16_pair(bb);
         }
+        // The A fragments of slice j + 1 are requested before slice j's dequantisation and matrix
+        // instructions (two register sets), so that LDS latency overlaps them instead of stalling
+        // every instruction on its own read.  The 64-column shapes (more waves per SIMD) have
+        // no registers for the second set and read each fragment where it is used.
+        if constexpr (SW == 1) {
+#pragma unroll
+            for (int j = 0; j < kSlices; ++j) {
+                f16x8_t bf[NF];
+#pragma unroll
+                for (int f = 0; f < NF; ++f) bf[f] = dequant_pairs(w.q[f][j], s2[f], b2[f], kMask, kMagic);
+                const char *ab = xring + buf * kBuf + xa[j];
+#pragma unroll
+                for (int a = 0; a < MF; ++a) {
+                    const f16x8_t af = *reinterpret_cast<const f16x8_t *>(ab + a * 16 * kUnits * 16);
+#pragma unroll
+                    for (int f = 0; f < NF; ++f)
+                        acc[a][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[f], acc[a][f], 0, 0, 0);
+                }
+            }
+            return;
+        }
+        f16x8_t af[2][MF];
+        auto read_a = [&](int j, f16x8_t *dst) {
+            const char *ab = xring + buf * kBuf + xa[j];
+#pragma unroll
+            for (int a = 0; a < MF; ++a) dst[a] = *reinterpret_cast<const f16x8_t *>(ab + a * 16 * kUnits * 16);
+        };
+        read_a(0, af[0]);
 #pragma unroll
         for (int j = 0; j < kSlices; ++j) {
+            if (j + 1 < kSlices) read_a(j + 1, af[(j + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
             f16x8_t bf[NF];
 #pragma unroll
             for (int f = 0; f < NF; ++f) bf[f] = dequant_pairs(w.q[f][j], s2[f], b2[f], kMask, kMagic);
-            const char *ab = lds + buf * kBuf + xa[j];
 #pragma unroll
-            for (int a = 0; a < MF; ++a) {
-                const f16x8_t af = *reinterpret_cast<const f16x8_t *>(ab + a * 16 * kUnits * 16);
+            for (int a = 0; a < MF; ++a)
 #pragma unroll
                 for (int f = 0; f < NF; ++f)
-                    acc[a][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[f], acc[a][f], 0, 0, 0);
-            }
+                    acc[a][f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[j & 1][a], bf[f], acc[a][f], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -294,29 +335,33 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
         // loads issued after the X slice of a step: its weights and the later D - 1 (X, weights) pairs
         constexpr int kAfterX = kWLoads + (D - 1) * (XI + kWLoads);
         WRegs w[NB];
-        // Requests past the last step are clamped to step GS - 1 (in bounds, never used), so
-        // that every step issues the same loads and the waits are fixed counts.
+        // Step i of this group is g_begin + kg + i * KW.  Requests past the last step are clamped
+        // to step GS - 1 (in bounds, never used), so that every step issues the same loads and the
+        // waits are fixed counts; all groups run the same number of steps (barriers), a group
+        // whose step lies beyond the range skips its compute.
+        const uint32_t nsteps = (g_end - g_begin + KW - 1) / KW;
+        auto gstep = [&](uint32_t i) { return g_begin + kg + i * KW; };
         auto gc = [&](uint32_t g) { return min(g, GS - 1); };
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            dma_x(gc(g_begin + d), d);
+            dma_x(gc(gstep(d)), d);
             __builtin_amdgcn_sched_barrier(0);  // X before the weights (vmcnt order)
-            load_w(gc(g_begin + d), w[d]);
+            load_w(gc(gstep(d)), w[d]);
             __builtin_amdgcn_sched_barrier(0);
         }
         asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfterX) : "memory");
         convert_x(0);
         __syncthreads();
-        auto step = [&](auto I, uint32_t g) {
-            constexpr int i = decltype(I)::value;
-            constexpr int pf = (i + D) % NB;
-            dma_x(gc(g + D), pf);
+        auto step = [&](auto I, uint32_t i) {
+            constexpr int b = decltype(I)::value;
+            constexpr int pf = (b + D) % NB;
+            dma_x(gc(gstep(i + D)), pf);
             __builtin_amdgcn_sched_barrier(0);
-            load_w(gc(g + D), w[pf]);
+            load_w(gc(gstep(i + D)), w[pf]);
             __builtin_amdgcn_sched_barrier(0);  // keep the loads at the top of the step
-            compute(i, w[i]);
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfterX) : "memory");  // X slice of step g + 1
-            convert_x((i + 1) % NB);
+            if (KW == 1 || gstep(i) < g_end) compute(b, w[b]);
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfterX) : "memory");  // X slice of the next step
+            convert_x((b + 1) % NB);
             __syncthreads();
         };
         using S0 = std::integral_constant<int, 0>;
@@ -324,19 +369,42 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
         using S2 = std::integral_constant<int, 2>;
         using S3 = std::integral_constant<int, 3>;
         static_assert(NB >= 2 && NB <= 4, "look-ahead of 1 to 3 steps");
-        uint32_t g = g_begin;
-        for (; g + NB <= g_end; g += NB) {
-            step(S0{}, g);
-            step(S1{}, g + 1);
-            if constexpr (NB > 2) step(S2{}, g + 2);
-            if constexpr (NB > 3) step(S3{}, g + 3);
+        uint32_t i = 0;
+        for (; i + NB <= nsteps; i += NB) {
+            step(S0{}, i);
+            step(S1{}, i + 1);
+            if constexpr (NB > 2) step(S2{}, i + 2);
+            if constexpr (NB > 3) step(S3{}, i + 3);
         }
-        if (g < g_end) step(S0{}, g);
+        if (i < nsteps) step(S0{}, i);
         if constexpr (NB > 2) {
-            if (g + 1 < g_end) step(S1{}, g + 1);
+            if (i + 1 < nsteps) step(S1{}, i + 1);
         }
         if constexpr (NB > 3) {
-            if (g + 2 < g_end) step(S2{}, g + 2);
+            if (i + 2 < nsteps) step(S2{}, i + 2);
+        }
+    }
+    if constexpr (KW > 1) {
+        // Groups 1 .. KW-1 hand their accumulators to group 0 through LDS (past the flag bytes of
+        // block_any; the last step's barrier ended every read of the X buffers), which adds them
+        // in group order.
+        constexpr int kAccBytes = MF * NF * 64 * 16;  // one wave's accumulators
+        static_assert(256 + (KW - 1) * WAVES * kAccBytes <= KW * (D + 1) * kBuf, "reduction area");
+        f32x4 *red = reinterpret_cast<f32x4 *>(lds + 256);
+        if (kg > 0) {
+#pragma unroll
+            for (int a = 0; a < MF; ++a)
+#pragma unroll
+                for (int f = 0; f < NF; ++f) red[(((kg - 1) * WAVES + wave) * MF * NF + a * NF + f) * 64 + lane] = acc[a][f];
+        }
+        __syncthreads();
+        if (kg == 0) {
+#pragma unroll
+            for (int k = 1; k < KW; ++k)
+#pragma unroll
+                for (int a = 0; a < MF; ++a)
+#pragma unroll
+                    for (int f = 0; f < NF; ++f) acc[a][f] += red[(((k - 1) * WAVES + wave) * MF * NF + a * NF + f) * 64 + lane];
         }
     }
     // Exact fallback (see the top of the file): a non-finite accumulator sends the block to a plain f32
@@ -348,10 +416,11 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
         for (int f = 0; f < NF; ++f)
 #pragma unroll
             for (int v = 0; v < 4; ++v) bad |= !__builtin_isfinite(acc[a][f][v]);
+    bad = bad && kg == 0;  // group 0 holds the sums
     if (block_any(bad)) {
         const uint32_t c0 = g_begin * 64 * SW, c1 = min(g_end * SW, G) * 64;
         const uint32_t outs = T::kBM * T::kBN;
-        for (uint32_t o = (uint32_t)tid; o < outs; o += 64 * WAVES) {
+        for (uint32_t o = (uint32_t)tid; o < outs; o += T::kThreads) {
             const uint32_t mi = o / T::kBN, ni = o % T::kBN;
             const uint32_t m = m0 + mi;
             const uint32_t fw = ni / T::kWaveRows, fr = ni % T::kWaveRows;  // wave, row of its fragments
@@ -397,46 +466,112 @@ __global__ __launch_bounds__(64 * WAVES, OCC) void q4_prefill_kernel(MfmaArgs ar
         return;
     }
 
-    // ---- epilogue: lane holds C[4 * kq + v][c] of each 16 x 16 fragment
+    // ---- epilogue.  A lane holds C[4 kq + v][c] of each 16 x 16 fragment: column pieces of 2 or 4
+    // bytes.  The block's tile goes through LDS (past block_any's flag bytes; every read of the X
+    // buffers and of the group reduction ended at a barrier) so that each thread then stores 8
+    // consecutive columns of one row: one 16-byte store for bf16, two for f32.
+    constexpr int kPitch = T::kBN + 4;  // floats per LDS row: 4 rows of a 16-column write hit distinct banks
+    constexpr bool kPartial = EPI == kMfmaPartial;
+    constexpr int kRows = (kPartial && NW == 2) ? 2 * T::kBM : T::kBM;  // partials: gate rows, then up rows
+    float *tile = reinterpret_cast<float *>(lds + 256);
+    if (kg == 0) {
 #pragma unroll
-    for (int fo = 0; fo < FPM; ++fo) {
-        const uint32_t n = row0 + fo * 16 + c;
-        if (n >= N) continue;
-        const float bias = (EPI == kMfmaDirect && P.bias) ? bf16_to_f32(P.bias[n]) : 0.0f;
+        for (int fo = 0; fo < FPM; ++fo) {
+            const int col = wave * T::kWaveRows + fo * 16 + c;
 #pragma unroll
-        for (int a = 0; a < MF; ++a) {
+            for (int a = 0; a < MF; ++a)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const uint32_t m = m0 + a * 16 + 4 * kq + v;
-                if (m >= M) continue;
-                const float g0 = acc[a][fo][v];
-                const float u0 = NW == 2 ? acc[a][fo + FPM][v] : 0.0f;
-                if (EPI == kMfmaPartial) {
-                    float *dst = args.partial + ((size_t)ks * M + m) * (size_t)(NW * N) + n;
-                    dst[0] = g0;
-                    if (NW == 2) dst[N] = u0;
-                    continue;
+                for (int v = 0; v < 4; ++v) {
+                    const int row = a * 16 + 4 * kq + v;
+                    const float g0 = acc[a][fo][v];
+                    if constexpr (kPartial) {
+                        tile[row * kPitch + col] = g0;
+                        if constexpr (NW == 2) tile[(T::kBM + row) * kPitch + col] = acc[a][fo + FPM][v];
+                    } else {
+                        tile[row * kPitch + col] = NW == 2 ? activation(g0, args.act) * acc[a][fo + FPM][v] : g0;
+                    }
                 }
-                float val = g0;
-                if (NW == 2) val = activation(val, args.act) * u0;
-                val += bias;
-                const size_t o = (size_t)m * P.ldo + n;
-                if (args.out_f32) {
-                    float *out = reinterpret_cast<float *>(P.out);
-                    out[o] = args.accumulate ? out[o] + val : val;
-                } else {
-                    uint16_t *out = reinterpret_cast<uint16_t *>(P.out);
-                    out[o] = (uint16_t)f32_to_bf16(args.accumulate ? val + bf16_to_f32(out[o]) : val);
+        }
+    }
+    __syncthreads();
+    const uint32_t n_base = nt * T::kBN;
+    const bool vec_out = kPartial ? ((uintptr_t)args.partial % 16 == 0 && N % 8 == 0)
+                                  : ((uintptr_t)P.out % 16 == 0 && P.ldo % 8 == 0 &&
+                                     (!(EPI == kMfmaDirect && P.bias) || (uintptr_t)P.bias % 16 == 0));
+    constexpr int kUnitsPerRow = T::kBN / 8;
+    for (uint32_t it = (uint32_t)tid; it < (uint32_t)(kRows * kUnitsPerRow); it += T::kThreads) {
+        const uint32_t r = it / kUnitsPerRow, cu = it % kUnitsPerRow;
+        const uint32_t row = r % T::kBM;
+        const uint32_t m = m0 + row, n = n_base + cu * 8;
+        if (m >= M || n >= N) continue;
+        const float *src = tile + r * kPitch + cu * 8;
+        float val[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) val[e] = src[e];
+        const bool full = vec_out && n + 8 <= N;
+        if constexpr (kPartial) {
+            float *dst = args.partial + ((size_t)ks * M + m) * (size_t)(NW * N) + (r / T::kBM) * N + n;
+            if (full) {
+                reinterpret_cast<f32x4 *>(dst)[0] = f32x4{val[0], val[1], val[2], val[3]};
+                reinterpret_cast<f32x4 *>(dst)[1] = f32x4{val[4], val[5], val[6], val[7]};
+            } else {
+                for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = val[e];
+            }
+            continue;
+        }
+        const size_t o = (size_t)m * P.ldo + n;
+        if (full) {
+            if (EPI == kMfmaDirect && P.bias) {
+                const u32x4 bw = *reinterpret_cast<const u32x4 *>(P.bias + n);
+                const uint32_t bb[4] = {bw.x, bw.y, bw.z, bw.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) val[e] += bf16_to_f32((bb[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+            }
+            if (args.out_f32) {
+                f32x4 *out = reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(P.out) + o);
+                f32x4 lo = {val[0], val[1], val[2], val[3]}, hi = {val[4], val[5], val[6], val[7]};
+                if (args.accumulate) {
+                    lo += out[0];
+                    hi += out[1];
                 }
+                out[0] = lo;
+                out[1] = hi;
+            } else {
+                u32x4 *out = reinterpret_cast<u32x4 *>(reinterpret_cast<uint16_t *>(P.out) + o);
+                if (args.accumulate) {
+                    const u32x4 ow = out[0];
+                    const uint32_t oo[4] = {ow.x, ow.y, ow.z, ow.w};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) val[e] += bf16_to_f32((oo[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+                }
+                uint32_t pk[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) pk[e] = f32_to_bf16(val[2 * e]) | (f32_to_bf16(val[2 * e + 1]) << 16);
+                out[0] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+            }
+            continue;
+        }
+        for (int e = 0; e < 8 && n + e < N; ++e) {
+            float x = val[e];
+            if (EPI == kMfmaDirect && P.bias) x += bf16_to_f32(P.bias[n + e]);
+            if (args.out_f32) {
+                float *out = reinterpret_cast<float *>(P.out);
+                out[o + e] = args.accumulate ? out[o + e] + x : x;
+            } else {
+                uint16_t *out = reinterpret_cast<uint16_t *>(P.out);
+                out[o + e] = (uint16_t)f32_to_bf16(args.accumulate ? x + bf16_to_f32(out[o + e]) : x);
             }
         }
     }
 }
 
-template <int MF, int NF, int WAVES, int NW, int OCC, int D, int SW>
+template <int MF, int NF, int WAVES, int NW, int OCC, int D, int SW, int KW = 1>
 static hipError_t launch_prefill_shape(MfmaArgs &a, hipStream_t s) {
-    using T = PrefillTile<MF, NF, WAVES, NW>;
-    constexpr int kLds = (D + 1) * T::kBM * 128 * SW;
+    using T = PrefillTile<MF, NF, WAVES, NW, KW>;
+    constexpr int kRing = KW * (D + 1) * T::kBM * 128 * SW;
+    constexpr int kTile = 256 + T::kBM * (T::kBN + 4) * 4;  // the epilogue's tile (gate/up partials: two)
+    constexpr int kLds = kRing > kTile ? kRing : kTile;
+    constexpr int kLdsPartial = kRing > kTile + (NW - 1) * (kTile - 256) ? kRing : kTile + (NW - 1) * (kTile - 256);
     uint32_t tiles = 0;
     const uint32_t tiles_m = (a.m + T::kBM - 1) / T::kBM;
     for (int i = 0; i < a.np; ++i) {
@@ -447,13 +582,13 @@ static hipError_t launch_prefill_shape(MfmaArgs &a, hipStream_t s) {
     if (a.groups_per_split % SW != 0) return hipErrorInvalidValue;
     const dim3 grid(tiles, a.ksplit > 1 ? a.ksplit : 1);
     if (a.ksplit > 1) {
-        hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaPartial, D, SW>), grid, dim3(T::kThreads),
-                           kLds, s, a);
+        hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaPartial, D, SW, KW>), grid, dim3(T::kThreads),
+                           kLdsPartial, s, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         return launch_splitk_reduce(a, NW, s);
     }
-    hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaDirect, D, SW>), grid, dim3(T::kThreads), kLds, s,
+    hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaDirect, D, SW, KW>), grid, dim3(T::kThreads), kLds, s,
                        a);
     return hipGetLastError();
 }
@@ -495,6 +630,11 @@ hipError_t launch_prefill(MfmaArgs &a, hipStream_t s) {
     }
     if (gate_up) return launch_prefill_shape<8, 2, 4, 2, 2, 1, 2>(a, s);
     if (a.ksplit > 1) return launch_prefill_shape<6, 2, 4, 1, 2, 1, 2>(a, s);
+    // Fewer tiles than two per compute unit (the N = 2048 .. 2560 projections at M = 512): two
+    // groups of waves per tile split its steps (qkv 20.2 -> 19.0 us; four groups: 21.8 us).
+    uint32_t tiles = 0;
+    for (int i = 0; i < a.np; ++i) tiles += ((a.m + 63) / 64) * ((a.p[i].w.n + 63) / 64);
+    if (tiles < 2u * (uint32_t)device_cus()) return launch_prefill_shape<4, 1, 4, 1, 2, 1, 2, 2>(a, s);
     return launch_prefill_shape<4, 1, 4, 1, 4, 1, 2>(a, s);
 }
 
