@@ -101,7 +101,7 @@ __device__ __forceinline__ uint32_t xs_index(uint32_t r, uint32_t u) {
 // kGateUp: interleaved gate/up tiles with the activation epilogue;
 // kGrouped: MoE expert groups.
 template <bool kGateUp, bool kGrouped>
-__global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void q4_skinny_kernel(
+__global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_eu(kGrouped ? 4 : 2))) void q4_skinny_kernel(
     SkinnyArgs a) {
     constexpr int NW = kSkinnyWaves;
     constexpr int KW = kSkinnyPieces;                  // 128-column pieces per wave
@@ -364,6 +364,24 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     };
 
     const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+    // Dense mode: the wave's X fragments do not change between the tiles of the run, so they are
+    // read from LDS once, with their group sums S (the same X fragments times a fragment of ones):
+    // 48 more registers (2 waves per SIMD), cfg1 B = 16 MLP 26.4 -> 24.9 us.  Grouped mode stages X
+    // per expert and keeps 4 waves per SIMD: it reads them per tile (119 against 129 us at T = 64).
+    constexpr bool kXRegs = !kGrouped;
+    bf16x8_t xf[KW][2][2];
+    f32x4 xsum[KW][2];
+    auto load_x_frags = [&]() {
+        const f32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < KW; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                xread2(i, h, xf[i][h]);
+                f32x4 sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[i][h][0], ones, zero, 0, 0, 0);
+                xsum[i][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[i][h][1], ones, sx, 0, 0, 0);
+            }
+    };
     auto tile_mma = [&](auto BUF) -> f32x4 {
         constexpr int b = decltype(BUF)::value;
         f32x4 acc = {0, 0, 0, 0};
@@ -381,13 +399,26 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
                 const float sg = __uint_as_float(h ? (sv & 0xFFFF0000u) : (sv << 16));
                 const float cg = fmaf(-128.0f, sg, __uint_as_float(h ? (bv & 0xFFFF0000u) : (bv << 16)));
                 bf16x8_t xp[2];
-                xread2(i, h, xp);
+                f32x4 sx;
+                if constexpr (kXRegs) {
+                    xp[0] = xf[i][h][0];
+                    xp[1] = xf[i][h][1];
+                } else {
+                    xread2(i, h, xp);
+                }
                 f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[0], q_frag(p01[h], kMask, kMagic), zero, 0, 0, 0);
-                f32x4 sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[0], ones, zero, 0, 0, 0);
+                if constexpr (!kXRegs) sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[0], ones, zero, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[1], q_frag(p23[h], kMask, kMagic), d, 0, 0, 0);
-                sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[1], ones, sx, 0, 0, 0);
+                if constexpr (kXRegs) {
+                    sx = xsum[i][h];
+                } else {
+                    sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[1], ones, sx, 0, 0, 0);
+                }
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[v] = fmaf(cg, sx[v], fmaf(sg, d[v], acc[v]));
+                // pinned here: otherwise the compiler sinks the arithmetic into the epilogue's
+                // conditional block and keeps every matrix result alive until then
+                asm volatile("" : "+v"(acc));
             }
         }
         return acc;
@@ -549,6 +580,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         if (a.ln_w) norm_x(rows);
         stage_store(rows);
         lds_barrier();
+        load_x_frags();
         // first tile of the problem after the one holding t (constant kernel-argument indices)
         auto next_begin = [&](uint32_t t) -> uint32_t {
             if (a.nmore > 0 && t < a.tile_begin[1]) return a.tile_begin[1];
