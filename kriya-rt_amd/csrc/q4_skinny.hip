@@ -86,10 +86,14 @@ __device__ __forceinline__ bf16x8_t q_frag(uint32_t w, uint32_t mask, uint32_t m
     return __builtin_bit_cast(bf16x8_t, r);
 }
 
-// LDS position of 16-byte X unit u (8 columns) of row r (XOR swizzle by row).
+// XOR swizzle of row r's 16-byte units: the 16 rows of a fragment read hit distinct banks
+// (r & 15 alone measured 35-42 % bank-conflict cycles for these reads; this order, none).
+__device__ __forceinline__ uint32_t xs_swz(uint32_t r) { return ((r & 7u) << 1) | ((r >> 3) & 1u); }
+
+// LDS position of 16-byte X unit u (8 columns) of row r (r < 16).
 template <int kUnits>
 __device__ __forceinline__ uint32_t xs_index(uint32_t r, uint32_t u) {
-    return r * kUnits + (u ^ r);
+    return r * kUnits + (u ^ xs_swz(r));
 }
 
 }  // namespace
@@ -200,7 +204,9 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     u32x4 wv[2][KW];
     uint32_t sp[2][KW], bp[2][KW];
     uint32_t pre_b[2] = {0, 0}, pre_o[2] = {0, 0};  // raw bits: converted at use, not at arrival
-    const uint32_t erow = (uint32_t)tid >> 4, ecol = (uint32_t)tid & 15u;  // epilogue output of threads < 256
+    // epilogue output (token row erow, column ecol) of threads < 256; the 64 threads of a wave read
+    // one v row of the reduction buffer (64 consecutive floats: no bank conflicts)
+    const uint32_t erow = 4u * (((uint32_t)tid >> 4) & 3u) + (((uint32_t)tid >> 6) & 3u), ecol = (uint32_t)tid & 15u;
     uint32_t orow = 0;                                                      // its output row (per segment)
     bool eout = false;                                                      // it stores an output
     // The epilogue's operands of tile t: unconditional loads (threads without an operand read
@@ -341,13 +347,13 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
 
     // X fragments of piece i for its four matrix instructions (h = group 2p + h, q = words 2q, 2q + 1):
     // lane group g reads unit 16 (p0 + i) + 4 (g & 1) + (g >> 1) + 2 q + 8 h of row r16, i.e.
-    // (swizzle) r16 * kUnits + 16 (p0 + i) + (unit ^ r16): one base per (h, q), and i as an immediate
+    // (swizzle) r16 * kUnits + 16 (p0 + i) + (unit ^ xs_swz(r16)): one base per (h, q), and i as an immediate
     // offset.  The low 32 bits of a generic LDS pointer are its LDS offset.
     uint32_t xaddr[4];  // [2 h + q]
 #pragma unroll
     for (uint32_t hq = 0; hq < 4; ++hq) {
         const uint32_t unit = 4u * ((uint32_t)g & 1u) + ((uint32_t)g >> 1) + 2u * (hq & 1u) + 8u * (hq >> 1);
-        xaddr[hq] = (uint32_t)reinterpret_cast<uintptr_t>(&xs[(uint32_t)r16 * kUnits + 16u * p0 + (unit ^ (uint32_t)r16)]);
+        xaddr[hq] = (uint32_t)reinterpret_cast<uintptr_t>(&xs[(uint32_t)r16 * kUnits + 16u * p0 + (unit ^ xs_swz(r16))]);
     }
     // The two X fragments of group 2p + h of piece i: two reads in flight, one wait.
     auto xread2 = [&](int i, int h, bf16x8_t (&x)[2]) {
