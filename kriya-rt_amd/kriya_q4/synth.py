@@ -87,7 +87,7 @@ def q4_weight(n: int, k: int, seed: int):
     return qw, scales, biases
 
 
-# ---- shapes of the benchmark configurations (BASELINE.json "configs") ----
+# ---- shapes of the benchmark configurations (configs 0-4) ----
 HIDDEN, INTER, VOCAB = 2048, 11008, 151936
 Q_DIM, KV_DIM = 2048, 256
 MOE_EXPERTS, MOE_TOPK, MOE_INTER = 60, 4, 1408
