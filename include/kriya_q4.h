@@ -19,6 +19,14 @@
  *     scratch array is shared by every call on one GPU).
  *   - Results do not depend on the launch grid: every output element is
  *     reduced by one wavefront in a fixed order (no atomics on data).
+ *   - Activation range.  For m < 64 token rows (the GEMV and few-token
+ *     kernels) every bf16 x is multiplied exactly (bf16 products, f32 sums).
+ *     For m >= 64 (the prefill kernel) x is staged in fp16, as the reference's
+ *     M >= 64 kernels stage half (q4_gemm_and_moe.metal:2722-2724): exact for
+ *     |x| in [2^-14, 65504]; a tile whose sums overflow fp16 is recomputed in
+ *     f32 (exact), and values below 2^-14 keep fp16's subnormal precision
+ *     (absolute error <= 2^-25 per element).  Weights are rounded once to fp16
+ *     there (w = fma(q, s, b)); elsewhere they are exact.
  *
  * Weight format (kr_q4_matrix): the planar affine Q4_G64 triplet
  *   qw     u32  [n, k/8]   word w of row r holds elements 8w..8w+7 of that
