@@ -109,6 +109,10 @@ const char *kr_last_error(void);
                                            by a kernel without block barriers when there are <= 64 of
                                            them and D is a power of two from 8 to 256, 0 always by the
                                            general kernel (same bits) */
+#define KR_OPT_PREFILL_OPERANDS 14      /* kr_q4_mlp at m >= 64: 1 (default) x is converted to the prefill
+                                         * kernel's fp16 operand once per call and the gate/up launch writes
+                                         * the activation in that form as well; 0 every block converts its
+                                         * own X slices.  Bitwise the same results either way. */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 

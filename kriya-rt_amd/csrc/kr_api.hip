@@ -309,6 +309,10 @@ int kr_set_option(int option, int value) {
             if (value != 0 && value != 1) return fail(KR_E_INVALID, "attention merge must be 0 or 1");
             tuning().attn_merge_wave = value;
             return ok();
+        case KR_OPT_PREFILL_OPERANDS:
+            if (value != 0 && value != 1) return fail(KR_E_INVALID, "prefill operands must be 0 or 1");
+            tuning().prefill_operands = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -328,6 +332,7 @@ int kr_get_option(int option) {
         case KR_OPT_GEMV_LONG_GROUPS: return tuning().gemv_long_groups;
         case KR_OPT_SPLITK_TICKETS: return tuning().splitk_tickets;
         case KR_OPT_ATTN_MERGE_WAVE: return tuning().attn_merge_wave;
+        case KR_OPT_PREFILL_OPERANDS: return tuning().prefill_operands;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -497,17 +502,27 @@ int kr_q4_qkv(const kr_q4_matrix *q, const kr_q4_matrix *k, const kr_q4_matrix *
 
 // MLP workspace layout: the tickets of the in-launch split-K reduction first, at the same place for
 // every m (zero between calls, so a workspace can serve several m), then the bf16 activation
-// [m, inter], then (m > 1) the f32 split-K partials of the down projection.
+// [m, inter], then (m > 1) the f32 split-K partials of the down projection, then (m on the prefill
+// kernel) x and the activation converted to the prefill kernel's fp16 operand order.
 constexpr size_t kMlpTicketBytes = ((size_t)kSkinnyTickets * 4 + 255) / 256 * 256;
 static uint32_t *mlp_ws_tickets(void *ws) { return (uint32_t *)ws; }
 static uint16_t *mlp_ws_act(void *ws) { return (uint16_t *)((char *)ws + kMlpTicketBytes); }
 static float *mlp_ws_partial(void *ws, uint32_t m, uint32_t inter) {
     return (float *)((char *)ws + kMlpTicketBytes + round_up((size_t)m * inter * 2, 256));
 }
+static bool mlp_prefill_operands(uint32_t m) { return m > kSkinnyChunkMaxM; }
+static uint16_t *mlp_ws_xh(void *ws, uint32_t m, uint32_t hidden, uint32_t inter) {
+    return (uint16_t *)((char *)mlp_ws_partial(ws, m, inter) + partial_bytes(m, hidden, inter, 1));
+}
+static uint16_t *mlp_ws_acth(void *ws, uint32_t m, uint32_t hidden, uint32_t inter) {
+    return (uint16_t *)((char *)mlp_ws_xh(ws, m, hidden, inter) + round_up((size_t)m * hidden * 2, 256));
+}
 
 size_t kr_q4_mlp_workspace_bytes(uint32_t m, uint32_t hidden, uint32_t intermediate) {
     size_t bytes = kMlpTicketBytes + round_up((size_t)m * intermediate * 2, 256);
     if (m > 1) bytes += partial_bytes(m, hidden, intermediate, 1);  // split-K partials of the down projection
+    if (mlp_prefill_operands(m))  // fp16 operands of the prefill kernel
+        bytes += round_up((size_t)m * hidden * 2, 256) + round_up((size_t)m * intermediate * 2, 256);
     return bytes;
 }
 
@@ -558,6 +573,31 @@ int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matr
         return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
     if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
     uint16_t *act = mlp_ws_act(workspace);
+    if (mlp_prefill_operands(m) && tuning().prefill_kernel != 1 && tuning().prefill_operands) {
+        // Prefill kernel for both: x converted to its fp16 operand order once (not once per block),
+        // and the gate/up epilogue writes the activation in that form too for the down projection
+        // (the bf16 activation stays the exact operand of the kernel's overflow fallback).
+        const Q4Mat g = to_mat(gate), u = to_mat(up);
+        hipStream_t s = (hipStream_t)stream;
+        MfmaArgs gu = mfma_args(x, m, gate->k, KR_DTYPE_BF16, 0);
+        gu.act = activation;
+        gu.p[0] = problem(g, &u, act, nullptr, gate->n);
+        gu.np = 1;
+        MfmaArgs dn = mfma_args(act, m, down->k, h_dtype, 1);
+        dn.p[0] = problem(to_mat(down), nullptr, h, nullptr, down->n);
+        dn.np = 1;
+        if (prefill_supported(gu) && prefill_supported(dn)) {
+            uint16_t *xh = mlp_ws_xh(workspace, m, gate->k, gate->n);
+            uint16_t *acth = mlp_ws_acth(workspace, m, gate->k, gate->n);
+            if (int rc = hip_status(launch_x_to_f16(x, m, gate->k, xh, s), "kr_q4_mlp (x to fp16)")) return rc;
+            gu.xh = xh;
+            gu.out_h = acth;
+            if (int rc = hip_status(launch_prefill(gu, s), "kr_q4_mlp (gate/up)")) return rc;
+            dn.xh = acth;
+            choose_split_k(dn, bm_class(m), mlp_ws_partial(workspace, m, gate->n));
+            return hip_status(launch_prefill(dn, s), "kr_q4_mlp (down)");
+        }
+    }
     if (int rc = kr_q4_gate_up_act(gate, up, x, m, act, KR_DTYPE_BF16, activation, stream)) return rc;
     return mlp_down(gate, down, act, h, h_dtype, m, workspace, stream);
 }

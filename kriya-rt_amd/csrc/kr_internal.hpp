@@ -42,6 +42,7 @@ struct Tuning {
     int splitk_tickets = 1;            // few-token split K: 1 the last block of a run reduces, 0 a second launch
     int attn_merge_wave = 1;           // decode attention merge of <= 64 slices, D a power of two 8..256:
                                        // 1 the barrier-free wave kernel, 0 the general block kernel
+    int prefill_operands = 1;          // kr_q4_mlp at m >= 64: 1 fp16 operands converted once per call
 };
 Tuning &tuning();
 
@@ -83,6 +84,13 @@ struct MfmaArgs {
     float *partial;         // split-K partials [ksplit, m, nw * N] (ksplit > 1)
     uint32_t ksplit;
     uint32_t groups_per_split;
+    // prefill kernel only (ignored elsewhere): x already converted to fp16 in the kernel's column
+    // order (launch_x_to_f16), read instead of converting x per block; x stays the exact operand
+    // of the overflow fallback
+    const uint16_t *xh;
+    // prefill gate/up with bf16 output only: also write the output converted the same way (the
+    // next projection's xh), [m, ldo] fp16
+    uint16_t *out_h;
 };
 
 // bm: the M tile class (16, 64 or 128) chosen by the caller from m.
@@ -90,6 +98,9 @@ hipError_t launch_mfma(MfmaArgs &a, int bm, hipStream_t s);
 // Prefill kernel (q4_prefill.hip): m > 16, k % 64 == 0, operands < 4 GiB.
 bool prefill_supported(const MfmaArgs &a);
 hipError_t launch_prefill(MfmaArgs &a, hipStream_t s);
+// xh[m, k] = fp16 of bf16 x[m, k] (RNE; beyond 65504 -> inf), each 8 columns in the order
+// e0 e4 e1 e5 e2 e6 e3 e7 of the prefill kernel's operands.  k % 8 == 0, 16-byte aligned rows.
+hipError_t launch_x_to_f16(const uint16_t *x, uint32_t m, uint32_t k, uint16_t *xh, hipStream_t s);
 int device_cus();                               // compute units of the current device
 uint32_t prefill_block_m(bool gate_up);         // token rows per block
 uint32_t prefill_block_rows(bool gate_up);      // weight rows (per matrix) per block

@@ -204,7 +204,9 @@ __global__ __launch_bounds__(64 * WAVES * KW, OCC) void q4_prefill_kernel(MfmaAr
     auto swizzle = [](uint32_t r) -> uint32_t { return SW == 1 ? swz(r) : (((r & 7) << 1) | ((r >> 3) & 1)); };
     constexpr int XI = T::kBM * kUnits / 64 / WAVES;  // DMA instructions per wave per step
     static_assert(T::kBM * kUnits % (64 * WAVES) == 0, "X slice must split into whole DMA instructions");
-    const rsrc_t rx = make_rsrc(args.x, (M - 1) * args.ldx * 2 + K * 2);
+    // x in bf16, converted here; or (args.xh) converted once beforehand, staged as it is
+    const bool cvt = args.xh == nullptr;
+    const rsrc_t rx = make_rsrc(cvt ? args.x : args.xh, (M - 1) * args.ldx * 2 + K * 2);
     uint32_t xo[XI];
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
@@ -217,6 +219,7 @@ __global__ __launch_bounds__(64 * WAVES * KW, OCC) void q4_prefill_kernel(MfmaAr
         for (int i = 0; i < XI; ++i) dma16(rx, xring + buf * kBuf + (wave * XI + i) * 1024, xo[i], g * (128 * SW));
     };
     auto convert_x = [&](int buf) {
+        if (!cvt) return;
 #pragma unroll
         for (int i = 0; i < XI; ++i) {
             u32x4 *p = reinterpret_cast<u32x4 *>(xring + buf * kBuf + (wave * XI + i) * 1024 + lane * 16);
@@ -460,7 +463,12 @@ __global__ __launch_bounds__(64 * WAVES * KW, OCC) void q4_prefill_kernel(MfmaAr
                 out[oo] = args.accumulate ? out[oo] + val : val;
             } else {
                 uint16_t *out = reinterpret_cast<uint16_t *>(P.out);
-                out[oo] = (uint16_t)f32_to_bf16(args.accumulate ? val + bf16_to_f32(out[oo]) : val);
+                const uint32_t b = f32_to_bf16(args.accumulate ? val + bf16_to_f32(out[oo]) : val);
+                out[oo] = (uint16_t)b;
+                if (NW == 2 && args.out_h) {  // column n of its 8-column unit goes to 2 (n % 4) + (n % 8) / 4
+                    const _Float16 hv = (_Float16)bf16_to_f32(b);
+                    args.out_h[oo - n + (n & ~7u) + 2 * (n & 3u) + ((n & 7u) >> 2)] = __builtin_bit_cast(uint16_t, hv);
+                }
             }
         }
         return;
@@ -548,6 +556,8 @@ __global__ __launch_bounds__(64 * WAVES * KW, OCC) void q4_prefill_kernel(MfmaAr
 #pragma unroll
                 for (int e = 0; e < 4; ++e) pk[e] = f32_to_bf16(val[2 * e]) | (f32_to_bf16(val[2 * e + 1]) << 16);
                 out[0] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+                if (NW == 2 && args.out_h)  // the same 8 values as the next projection's fp16 operand
+                    *reinterpret_cast<u32x4 *>(args.out_h + o) = x_unit_f16(u32x4{pk[0], pk[1], pk[2], pk[3]});
             }
             continue;
         }
@@ -559,10 +569,32 @@ __global__ __launch_bounds__(64 * WAVES * KW, OCC) void q4_prefill_kernel(MfmaAr
                 out[o + e] = args.accumulate ? out[o + e] + x : x;
             } else {
                 uint16_t *out = reinterpret_cast<uint16_t *>(P.out);
-                out[o + e] = (uint16_t)f32_to_bf16(args.accumulate ? x + bf16_to_f32(out[o + e]) : x);
+                const uint32_t b = f32_to_bf16(args.accumulate ? x + bf16_to_f32(out[o + e]) : x);
+                out[o + e] = (uint16_t)b;
+                if (NW == 2 && args.out_h) {  // element e of its 8-column unit goes to 2 (e % 4) + e / 4
+                    const _Float16 hv = (_Float16)bf16_to_f32(b);
+                    const uint32_t c = n + e;
+                    args.out_h[o - n + (c & ~7u) + 2 * (c & 3u) + ((c & 7u) >> 2)] = __builtin_bit_cast(uint16_t, hv);
+                }
             }
         }
     }
+}
+
+// One 16-byte unit (8 columns) per thread.
+__global__ __launch_bounds__(256) void x_to_f16_kernel(const u32x4 *x, u32x4 *xh, uint32_t units) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < units) xh[i] = x_unit_f16(x[i]);
+}
+
+hipError_t launch_x_to_f16(const uint16_t *x, uint32_t m, uint32_t k, uint16_t *xh, hipStream_t s) {
+    if (k % 8 != 0 || (uintptr_t)x % 16 != 0 || (uintptr_t)xh % 16 != 0) return hipErrorInvalidValue;
+    const uint64_t units = (uint64_t)m * (k / 8);
+    if (units == 0) return hipSuccess;
+    if (units >= (1ull << 32)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(x_to_f16_kernel, dim3((uint32_t)((units + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<const u32x4 *>(x), reinterpret_cast<u32x4 *>(xh), (uint32_t)units);
+    return hipGetLastError();
 }
 
 template <int MF, int NF, int WAVES, int NW, int OCC, int D, int SW, int KW = 1>

@@ -35,6 +35,7 @@ OPT_MOE_GEMV = 10
 OPT_GEMV_LONG_GROUPS = 11
 OPT_SPLITK_TICKETS = 12
 OPT_ATTN_MERGE_WAVE = 13
+OPT_PREFILL_OPERANDS = 14
 
 _lib = None
 

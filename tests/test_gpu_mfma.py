@@ -188,3 +188,36 @@ def test_prefill_kernels_agree(kq, m):
     got = kq.q4_linear(w, x, out_dtype=kq.DTYPE_F32).cpu().numpy()
     for opt, ref in outs.items():
         assert np.max(np.abs(got - ref)) <= 1e-4 * rms(ref), f"option {opt}"
+
+
+@pytest.mark.parametrize("m", [64, 200])
+def test_mlp_prefill_operands_bitwise(kq, m):
+    """kr_q4_mlp at m >= 64 converts x to the prefill kernel's fp16 operands once and has the gate/up
+    launch write the activation in that form for the down projection: the same bits as every block
+    converting its own X slices (option 0), also when x overflows fp16 (the blocks whose sums do not
+    stay finite recompute their tiles in f32 from the bf16 operands) -- against the oracle as well."""
+    s = synth()
+    case(f"mlp m={m} hidden 512 inter 1408: pre-converted fp16 operands vs per-block conversion")
+    g, u = s.q4_weight(1408, 512, 2801), s.q4_weight(1408, 512, 2802)
+    d = s.q4_weight(512, 1408, 2803)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    lib = kq.lib()
+    xs = {"normal": s.bf16_normal((m, 512), 2804 + m)}
+    big = O.bf16_to_f32(xs["normal"]).copy()
+    big[3] *= 1e5  # a row beyond fp16's range (65504)
+    xs["overflow"] = O.f32_to_bf16(big)
+    for name, x in xs.items():
+        res = {}
+        try:
+            for opt in (0, 1):
+                assert lib.kr_set_option(kq.OPT_PREFILL_OPERANDS, opt) == 0
+                h = torch.zeros((m, 512), dtype=torch.float32, device="cuda")
+                kq.mlp(G, U, D, h, x=dev_bf16(x))
+                res[opt] = h.cpu().numpy()
+        finally:
+            lib.kr_set_option(kq.OPT_PREFILL_OPERANDS, 1)
+        assert np.array_equal(res[0].view(np.uint32), res[1].view(np.uint32)), name
+        want = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), x)
+        assert np.all(np.isfinite(res[1])), name
+        for i in range(m):
+            assert_rms_close(res[1][i], want[i], what=f"mlp {name} row {i}")
