@@ -113,6 +113,9 @@ const char *kr_last_error(void);
                                          * kernel's fp16 operand once per call and the gate/up launch writes
                                          * the activation in that form as well; 0 every block converts its
                                          * own X slices.  Bitwise the same results either way. */
+#define KR_OPT_SKINNY_GROUPS 15         /* few-token kernel, 17 <= m <= 63: 2 (default) 32-row launches, each
+                                         * multiplying every unpacked weight word with two 16-row groups
+                                         * of x; 1 16-row launches.  Bitwise the same results either way. */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 

@@ -104,16 +104,17 @@ MfmaProblem problem(const Q4Mat &w, const Q4Mat *w2, void *out, const uint16_t *
 // is needed when the K split exceeds one block; without it the caller must use
 // another path (returns hipErrorInvalidValue).  `tickets` (kSkinnyTickets zero
 // words, left zero): the split is reduced inside the launch, else by a second one.
-// More than 16 rows (up to kSkinnyChunkMaxM): 16-row chunks, one launch each, in row order; each
-// reuses the partials and leaves the tickets at zero for the next.
+// More than one launch's rows (32, or 16 with KR_OPT_SKINNY_GROUPS = 1; up to kSkinnyChunkMaxM):
+// chunks, one launch each, in row order; each reuses the partials and leaves the tickets at zero
+// for the next.
 hipError_t run_skinny(const Q4Mat &w, const Q4Mat *w2, const uint16_t *x, uint32_t m, void *out,
                       const uint16_t *bias, uint32_t ldo, int out_dtype, int accumulate, int act, float *partial,
                       hipStream_t s, const uint16_t *ln_w = nullptr, float eps = 0.0f,
                       uint32_t *tickets = nullptr) {
-    if (m > kSkinnyMaxM) {
+    if (const uint32_t chunk = skinny_chunk_rows(); m > chunk) {
         const size_t esz = dtype_size(out_dtype);
-        for (uint32_t i0 = 0; i0 < m; i0 += kSkinnyMaxM) {
-            const uint32_t mc = std::min(kSkinnyMaxM, m - i0);
+        for (uint32_t i0 = 0; i0 < m; i0 += chunk) {
+            const uint32_t mc = std::min(chunk, m - i0);
             if (hipError_t e = run_skinny(w, w2, x + (size_t)i0 * w.k, mc, (char *)out + (size_t)i0 * ldo * esz, bias, ldo,
                                           out_dtype, accumulate, act, partial, s, ln_w, eps, tickets))
                 return e;
@@ -162,13 +163,13 @@ hipError_t run_skinny(const Q4Mat &w, const Q4Mat *w2, const uint16_t *x, uint32
 hipError_t run_skinny_qkv(const kr_q4_matrix *const *mats, const uint16_t *const *biases, void *const *outs,
                           const uint16_t *x, uint32_t m, int out_dtype, const uint16_t *ln_w, float eps,
                           hipStream_t s) {
-    if (m > kSkinnyMaxM) {  // 16-row chunks, as run_skinny
+    if (const uint32_t chunk = skinny_chunk_rows(); m > chunk) {  // chunks, as run_skinny
         const size_t esz = dtype_size(out_dtype);
-        for (uint32_t i0 = 0; i0 < m; i0 += kSkinnyMaxM) {
+        for (uint32_t i0 = 0; i0 < m; i0 += chunk) {
             void *o[3];
             for (int i = 0; i < 3; ++i) o[i] = (char *)outs[i] + (size_t)i0 * mats[i]->n * esz;
             if (hipError_t e = run_skinny_qkv(mats, biases, o, x + (size_t)i0 * mats[0]->k,
-                                              std::min(kSkinnyMaxM, m - i0), out_dtype, ln_w, eps, s))
+                                              std::min(chunk, m - i0), out_dtype, ln_w, eps, s))
                 return e;
         }
         return hipSuccess;
@@ -313,6 +314,10 @@ int kr_set_option(int option, int value) {
             if (value != 0 && value != 1) return fail(KR_E_INVALID, "prefill operands must be 0 or 1");
             tuning().prefill_operands = value;
             return ok();
+        case KR_OPT_SKINNY_GROUPS:
+            if (value != 1 && value != 2) return fail(KR_E_INVALID, "few-token row groups must be 1 or 2");
+            tuning().skinny_groups = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -333,6 +338,7 @@ int kr_get_option(int option) {
         case KR_OPT_SPLITK_TICKETS: return tuning().splitk_tickets;
         case KR_OPT_ATTN_MERGE_WAVE: return tuning().attn_merge_wave;
         case KR_OPT_PREFILL_OPERANDS: return tuning().prefill_operands;
+        case KR_OPT_SKINNY_GROUPS: return tuning().skinny_groups;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }

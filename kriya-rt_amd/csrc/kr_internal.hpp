@@ -43,6 +43,7 @@ struct Tuning {
     int attn_merge_wave = 1;           // decode attention merge of <= 64 slices, D a power of two 8..256:
                                        // 1 the barrier-free wave kernel, 0 the general block kernel
     int prefill_operands = 1;          // kr_q4_mlp at m >= 64: 1 fp16 operands converted once per call
+    int skinny_groups = 2;             // dense few-token launches: 16-row groups per launch (1 or 2)
 };
 Tuning &tuning();
 
@@ -108,8 +109,10 @@ uint32_t prefill_block_rows(bool gate_up);      // weight rows (per matrix) per 
 hipError_t launch_splitk_reduce(const MfmaArgs &a, int nw, hipStream_t s);
 
 // ---- few-token (m <= 16) and grouped MoE matrix-core path (q4_skinny.hip)
-constexpr uint32_t kSkinnyMaxM = 16;
-constexpr uint32_t kSkinnyChunkMaxM = 63;  // the host runs 17..63 rows as 16-row chunks
+constexpr uint32_t kSkinnyMaxM = 32;       // rows of one dense launch (two groups of 16)
+constexpr uint32_t kSkinnyChunkMaxM = 63;  // the host runs 33..63 rows as 32-row chunks
+// Rows of one dense few-token launch under the current tuning.
+inline uint32_t skinny_chunk_rows() { return tuning().skinny_groups == 1 ? 16u : kSkinnyMaxM; }
 constexpr uint32_t kMaxExperts = 256;
 struct SkinnyArgs {
     Q4Mat w, w2;            // w2: up matrix for the gate/up epilogue (qw == nullptr otherwise)

@@ -103,17 +103,20 @@ __device__ __forceinline__ uint32_t xs_index(uint32_t r, uint32_t u) {
 // 128-column pieces w * kPieces .. + kPieces - 1 and the 8 waves' 16 x 16
 // partial products are summed through LDS in wave order.
 // kGateUp: interleaved gate/up tiles with the activation epilogue;
-// kGrouped: MoE expert groups.
-template <bool kGateUp, bool kGrouped>
+// kGrouped: MoE expert groups;
+// MG: groups of 16 token rows per launch (dense mode: 1 or 2).  With two, every unpacked weight
+// word is multiplied with both groups' X fragments (32 rows for the price of little more than 16).
+template <bool kGateUp, bool kGrouped, int MG>
 __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_eu(kGrouped ? 4 : 2))) void q4_skinny_kernel(
     SkinnyArgs a) {
+    static_assert(MG == 1 || (MG == 2 && !kGrouped), "two row groups in dense mode only");
     constexpr int NW = kSkinnyWaves;
     constexpr int KW = kSkinnyPieces;                  // 128-column pieces per wave
     constexpr uint32_t kTileRows = kGateUp ? 8 : 16;  // output features per tile
     constexpr int kUnits = NW * KW * 16;               // 16-byte X units per LDS row
     constexpr int kStage = 16 * kUnits / (NW * 64);    // X units staged per thread
     __shared__ u32x4 xs[16 * kUnits];                  // X slab: 16 rows x kSlabCols bf16
-    __shared__ float red[2][NW][4][64];                // per-wave partial tiles, double buffered
+    __shared__ float red[2][MG][NW][4][64];            // per-wave partial tiles, double buffered
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -204,9 +207,11 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     u32x4 wv[2][KW];
     uint32_t sp[2][KW], bp[2][KW];
     uint32_t pre_b[2] = {0, 0}, pre_o[2] = {0, 0};  // raw bits: converted at use, not at arrival
-    // epilogue output (token row erow, column ecol) of threads < 256; the 64 threads of a wave read
-    // one v row of the reduction buffer (64 consecutive floats: no bank conflicts)
-    const uint32_t erow = 4u * (((uint32_t)tid >> 4) & 3u) + (((uint32_t)tid >> 6) & 3u), ecol = (uint32_t)tid & 15u;
+    // epilogue output (token row erow, column ecol) of threads < 256 MG: row group tid / 256; the 64
+    // threads of a wave read one v row of the reduction buffer (64 consecutive floats: no bank
+    // conflicts)
+    const uint32_t erow = 16u * ((uint32_t)tid >> 8) + 4u * (((uint32_t)tid >> 4) & 3u) + (((uint32_t)tid >> 6) & 3u),
+                   ecol = (uint32_t)tid & 15u;
     uint32_t orow = 0;                                                      // its output row (per segment)
     bool eout = false;                                                      // it stores an output
     // The epilogue's operands of tile t: unconditional loads (threads without an operand read
@@ -268,8 +273,8 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     // requested the first tile's words) the conversion and LDS stores.
     // Loads are unconditional (dead units re-read row `base`, unit 0) and
     // zeroed after, so that no branch splits the batch of loads.
-    u32x4 raw[kStage];
-    auto stage_load = [&](uint32_t base, uint32_t rows) {
+    u32x4 raw[MG][kStage];  // [row group]
+    auto stage_load = [&](u32x4(&rw)[kStage], uint32_t base, uint32_t rows) {
 #pragma unroll
         for (int s = 0; s < kStage; ++s) {
             const uint32_t idx = (uint32_t)tid + (uint32_t)s * (NW * 64);
@@ -279,17 +284,17 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             if constexpr (kGrouped) {
                 if (a.x_div) xr = a.sorted[xr] / a.x_div;
             }
-            raw[s] = *reinterpret_cast<const u32x4 *>(a.x + (size_t)xr * a.ldx + k0 + 8 * (live ? u : 0u));
+            rw[s] = *reinterpret_cast<const u32x4 *>(a.x + (size_t)xr * a.ldx + k0 + 8 * (live ? u : 0u));
         }
     };
-    auto stage_store = [&](uint32_t rows) {
+    auto stage_store = [&](const u32x4(&rw)[kStage], uint32_t rows) {
 #pragma unroll
         for (int s = 0; s < kStage; ++s) {
             const uint32_t idx = (uint32_t)tid + (uint32_t)s * (NW * 64);
             const uint32_t r = idx / kUnits, u = idx % kUnits;
             const bool live = r < rows && u < npieces * 16;
             const u32x4 z = {0, 0, 0, 0};
-            xs[xs_index<kUnits>(r, u)] = x_unit(live ? raw[s] : z);
+            xs[xs_index<kUnits>(r, u)] = x_unit(live ? rw[s] : z);
         }
     };
 
@@ -301,9 +306,9 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     // tid / kUnits + 2 s, so one ln_w unit serves all of them.  Per-row sums of
     // squares: wave sums, then the four waves of a row parity in order.
     // (s_ss and s_scale live in the reduction buffer, unused until the first tile)
-    float (*s_ss)[4] = reinterpret_cast<float (*)[4]>(&red[0][0][0][0]);
-    float *s_scale = &red[1][0][0][0];
-    auto norm_x = [&](uint32_t rows) {
+    float (*s_ss)[4] = reinterpret_cast<float (*)[4]>(&red[0][0][0][0][0]);
+    float *s_scale = &red[1][0][0][0][0];
+    auto norm_x = [&](u32x4(&rw)[kStage], uint32_t rows) {
         static_assert(NW * 64 == 2 * kUnits, "two rows per staging round");
         const uint32_t u = (uint32_t)tid % kUnits, r0 = (uint32_t)tid / kUnits;
         const bool ulive = u < npieces * 16;
@@ -313,7 +318,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             const uint32_t r = r0 + 2u * (uint32_t)st;
             float ss = 0.0f;
             if (ulive && r < rows) {
-                const uint32_t X[4] = {raw[st].x, raw[st].y, raw[st].z, raw[st].w};
+                const uint32_t X[4] = {rw[st].x, rw[st].y, rw[st].z, rw[st].w};
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float lo = __uint_as_float(X[i] << 16), hi = __uint_as_float(X[i] & 0xFFFF0000u);
@@ -334,14 +339,14 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int st = 0; st < kStage; ++st) {
             const float scale = s_scale[r0 + 2u * (uint32_t)st];
-            uint32_t X[4] = {raw[st].x, raw[st].y, raw[st].z, raw[st].w};
+            uint32_t X[4] = {rw[st].x, rw[st].y, rw[st].z, rw[st].w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float lo = __uint_as_float(X[i] << 16) * scale * __uint_as_float(W[i] << 16);
                 const float hi = __uint_as_float(X[i] & 0xFFFF0000u) * scale * __uint_as_float(W[i] & 0xFFFF0000u);
                 X[i] = pack_bf16_rne(lo, hi);
             }
-            raw[st] = u32x4{X[0], X[1], X[2], X[3]};
+            rw[st] = u32x4{X[0], X[1], X[2], X[3]};
         }
     };
 
@@ -375,22 +380,28 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     // 48 more registers (2 waves per SIMD), cfg1 B = 16 MLP 26.4 -> 24.9 us.  Grouped mode stages X
     // per expert and keeps 4 waves per SIMD: it reads them per tile (119 against 129 us at T = 64).
     constexpr bool kXRegs = !kGrouped;
-    bf16x8_t xf[KW][2][2];
-    f32x4 xsum[KW][2];
-    auto load_x_frags = [&]() {
+    bf16x8_t xf[MG][KW][2][2];
+    f32x4 xsum[MG][KW][2];
+    auto load_x_frags = [&](auto GI) {  // into row group GI's registers
+        constexpr int gi = decltype(GI)::value;
         const f32x4 zero = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < KW; ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                xread2(i, h, xf[i][h]);
-                f32x4 sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[i][h][0], ones, zero, 0, 0, 0);
-                xsum[i][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[i][h][1], ones, sx, 0, 0, 0);
+                xread2(i, h, xf[gi][i][h]);
+                f32x4 sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[gi][i][h][0], ones, zero, 0, 0, 0);
+                xsum[gi][i][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf[gi][i][h][1], ones, sx, 0, 0, 0);
             }
     };
-    auto tile_mma = [&](auto BUF) -> f32x4 {
+    struct Acc {
+        f32x4 v[MG];
+    };
+    auto tile_mma = [&](auto BUF) -> Acc {
         constexpr int b = decltype(BUF)::value;
-        f32x4 acc = {0, 0, 0, 0};
+        Acc acc;
+#pragma unroll
+        for (int gi = 0; gi < MG; ++gi) acc.v[gi] = f32x4{0, 0, 0, 0};
         const f32x4 zero = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < KW; ++i) {
@@ -404,27 +415,31 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             for (int h = 0; h < 2; ++h) {  // one group at a time: fewer registers live
                 const float sg = __uint_as_float(h ? (sv & 0xFFFF0000u) : (sv << 16));
                 const float cg = fmaf(-128.0f, sg, __uint_as_float(h ? (bv & 0xFFFF0000u) : (bv << 16)));
-                bf16x8_t xp[2];
-                f32x4 sx;
-                if constexpr (kXRegs) {
-                    xp[0] = xf[i][h][0];
-                    xp[1] = xf[i][h][1];
-                } else {
-                    xread2(i, h, xp);
-                }
-                f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[0], q_frag(p01[h], kMask, kMagic), zero, 0, 0, 0);
-                if constexpr (!kXRegs) sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[0], ones, zero, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[1], q_frag(p23[h], kMask, kMagic), d, 0, 0, 0);
-                if constexpr (kXRegs) {
-                    sx = xsum[i][h];
-                } else {
-                    sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[1], ones, sx, 0, 0, 0);
-                }
+                const bf16x8_t q01 = q_frag(p01[h], kMask, kMagic), q23 = q_frag(p23[h], kMask, kMagic);
 #pragma unroll
-                for (int v = 0; v < 4; ++v) acc[v] = fmaf(cg, sx[v], fmaf(sg, d[v], acc[v]));
-                // pinned here: otherwise the compiler sinks the arithmetic into the epilogue's
-                // conditional block and keeps every matrix result alive until then
-                asm volatile("" : "+v"(acc));
+                for (int gi = 0; gi < MG; ++gi) {  // the unpacked words serve every row group
+                    bf16x8_t xp[2];
+                    f32x4 sx;
+                    if constexpr (kXRegs) {
+                        xp[0] = xf[gi][i][h][0];
+                        xp[1] = xf[gi][i][h][1];
+                    } else {
+                        xread2(i, h, xp);
+                    }
+                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[0], q01, zero, 0, 0, 0);
+                    if constexpr (!kXRegs) sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[0], ones, zero, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[1], q23, d, 0, 0, 0);
+                    if constexpr (kXRegs) {
+                        sx = xsum[gi][i][h];
+                    } else {
+                        sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xp[1], ones, sx, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) acc.v[gi][v] = fmaf(cg, sx[v], fmaf(sg, d[v], acc.v[gi][v]));
+                    // pinned here: otherwise the compiler sinks the arithmetic into the epilogue's
+                    // conditional block and keeps every matrix result alive until then
+                    asm volatile("" : "+v"(acc.v[gi]));
+                }
             }
         }
         return acc;
@@ -432,17 +447,19 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
 
     // ---- epilogue: output (erow, ecol) of the tile, summed over the waves in order
     int par = 0;
-    auto finish = [&](auto BUF, const f32x4 &acc, uint32_t t) {
+    auto finish = [&](auto BUF, const Acc &acc, uint32_t t) {
         constexpr int b = decltype(BUF)::value;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) red[par][wave][v][lane] = acc[v];
+        for (int gi = 0; gi < MG; ++gi)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[par][gi][wave][v][lane] = acc.v[gi][v];
         lds_barrier();
         const uint32_t f = kGateUp ? t * 8 + (ecol & 7) : t * 16 + ecol;
         if (eout && f < crows) {
-            const uint32_t L = 16u * (erow >> 2) + ecol, v = erow & 3u;
+            const uint32_t L = 16u * ((erow & 15u) >> 2) + ecol, v = erow & 3u, eg = MG > 1 ? erow >> 4 : 0u;
             float val = 0.0f;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) val += red[par][w][v][L];
+            for (int w = 0; w < NW; ++w) val += red[par][eg][w][v][L];
             if (a.partial) {  // dense split-K: [ksplit, m, nw * n], gate at f, up at n + f
                 const uint32_t nw = kGateUp ? 2 : 1;
                 float *dst = a.partial + ((size_t)slab * a.m + erow) * (size_t)(nw * crows);
@@ -454,7 +471,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
                 if constexpr (kGateUp) {
                     float up = 0.0f;
 #pragma unroll
-                    for (int w = 0; w < NW; ++w) up += red[par][w][v][L + 8];
+                    for (int w = 0; w < NW; ++w) up += red[par][eg][w][v][L + 8];
                     val = activation(val, a.act) * up;
                 }
                 if (cbias) val += bf16_to_f32(pre_b[b]);
@@ -500,7 +517,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     auto reduce_run = [&]() {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are done
         __syncthreads();
-        uint32_t *s_ticket = reinterpret_cast<uint32_t *>(&red[0][0][0][0]);  // red is free here
+        uint32_t *s_ticket = reinterpret_cast<uint32_t *>(&red[0][0][0][0][0]);  // red is free here
         const uint32_t rb = blockIdx.x / a.ksplit;
         // Ordering argument (a hardware one, not a C++ release/acquire pair).  The partials were
         // written with agent-scope relaxed atomic stores: on gfx950 these are global stores with
@@ -554,8 +571,8 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     };
 
     if constexpr (!kGrouped) {  // dense: one X for the whole run
-        const uint32_t rows = min(a.m, 16u);
-        eout = tid < 256 && erow < rows && (!kGateUp || a.partial || ecol < 8);
+        const uint32_t rows = min(a.m, 16u * MG);
+        eout = tid < 256 * MG && erow < rows && (!kGateUp || a.partial || ecol < 8);
         orow = erow;
         // the problem holding tile t: its fields, by value; returns its first tile
         auto select = [&](uint32_t t) -> uint32_t {
@@ -579,14 +596,25 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             return a.tile_begin[pi];
         };
         uint32_t tb = select(run_begin);
-        // X loads first, then the first tile's words: the conversion waits for X only
-        stage_load(0, rows);
+        // X loads first (every row group's), then the first tile's words: the conversion waits for
+        // X only.  The row groups pass through the one LDS slab in turn (the launcher gives a
+        // two-group launch more than 16 rows, so row 16 exists).
+        const uint32_t rows0 = min(rows, 16u), rows1 = rows - rows0;
+        stage_load(raw[0], 0, rows0);
+        if constexpr (MG == 2) stage_load(raw[MG - 1], 16, rows1);
         fetch(B0{}, 0, run_begin - tb);
         __builtin_amdgcn_sched_barrier(0);
-        if (a.ln_w) norm_x(rows);
-        stage_store(rows);
+        if (a.ln_w) norm_x(raw[0], rows0);
+        stage_store(raw[0], rows0);
         lds_barrier();
-        load_x_frags();
+        load_x_frags(std::integral_constant<int, 0>{});
+        if constexpr (MG == 2) {
+            lds_barrier();  // every wave has read group 0's fragments
+            if (a.ln_w) norm_x(raw[MG - 1], rows1);
+            stage_store(raw[MG - 1], rows1);
+            lds_barrier();
+            load_x_frags(std::integral_constant<int, MG - 1>{});
+        }
         // first tile of the problem after the one holding t (constant kernel-argument indices)
         auto next_begin = [&](uint32_t t) -> uint32_t {
             if (a.nmore > 0 && t < a.tile_begin[1]) return a.tile_begin[1];
@@ -619,11 +647,11 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             eout = tid < 256 && erow < rows && (!kGateUp || a.partial || ecol < 8);
             orow = base + c0 + erow;
             if (eout && a.out_scatter) orow = a.sorted[orow];
-            stage_load(base + c0, rows);
+            stage_load(raw[0], base + c0, rows);
             fetch(B0{}, e, t_begin);
             __builtin_amdgcn_sched_barrier(0);
             lds_barrier();  // the previous segment's readers are done with xs
-            stage_store(rows);
+            stage_store(raw[0], rows);
             lds_barrier();
             run_tiles(e, t_begin, t_end);
         }
@@ -633,7 +661,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
 
 namespace {
 
-template <bool GU, bool G>
+template <bool GU, bool G, int MG>
 hipError_t launch_t(SkinnyArgs &a, uint32_t items, hipStream_t s) {
     // blocks per slab: every CU busy, each block a contiguous run of ceil(items / nblk) tiles
     // grouped (MoE) launches take twice the cap: cfg4 T = 64 is 1.3 % faster at 512 blocks, the dense
@@ -643,7 +671,7 @@ hipError_t launch_t(SkinnyArgs &a, uint32_t items, hipStream_t s) {
     if (a.tickets) cap = std::min(cap, kSkinnyTickets);  // one ticket word per run
     const uint32_t nblk = std::max<uint32_t>(1, std::min(items, cap));
     const dim3 grid(nblk * a.ksplit), block(kSkinnyWaves * 64);
-    hipLaunchKernelGGL((q4_skinny_kernel<GU, G>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((q4_skinny_kernel<GU, G, MG>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 
@@ -661,6 +689,7 @@ hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s) {
     if (grouped && a.ksplit != 1) return hipErrorInvalidValue;
     if (grouped && (a.nmore > 0 || a.ln_w)) return hipErrorInvalidValue;
     if (a.nmore < 0 || a.nmore > 2 || (a.nmore > 0 && (gate_up || a.partial))) return hipErrorInvalidValue;
+    if (!grouped && (a.m == 0 || a.m > kSkinnyMaxM)) return hipErrorInvalidValue;
     if (a.ln_w && a.ksplit != 1) return hipErrorInvalidValue;  // the norm needs the whole row in the slab
     if (a.tickets && (grouped || a.nmore > 0 || !a.partial || a.ksplit < 2 || a.ksplit > kSkinnyMaxTicketSplit))
         return hipErrorInvalidValue;
@@ -677,8 +706,10 @@ hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s) {
     }
     const uint32_t items =
         grouped ? a.max_active * ((a.expert_rows + tile_rows - 1) / tile_rows) : a.tile_begin[a.nmore + 1];
-    if (gate_up) return grouped ? launch_t<true, true>(a, items, s) : launch_t<true, false>(a, items, s);
-    return grouped ? launch_t<false, true>(a, items, s) : launch_t<false, false>(a, items, s);
+    if (grouped) return gate_up ? launch_t<true, true, 1>(a, items, s) : launch_t<false, true, 1>(a, items, s);
+    if (a.m > 16)  // two row groups per launch
+        return gate_up ? launch_t<true, false, 2>(a, items, s) : launch_t<false, false, 2>(a, items, s);
+    return gate_up ? launch_t<true, false, 1>(a, items, s) : launch_t<false, false, 1>(a, items, s);
 }
 
 uint32_t skinny_ksplit(uint32_t k) { return (k + kSlabCols - 1) / kSlabCols; }

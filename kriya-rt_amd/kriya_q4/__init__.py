@@ -36,6 +36,7 @@ OPT_GEMV_LONG_GROUPS = 11
 OPT_SPLITK_TICKETS = 12
 OPT_ATTN_MERGE_WAVE = 13
 OPT_PREFILL_OPERANDS = 14
+OPT_SKINNY_GROUPS = 15
 
 _lib = None
 

@@ -221,3 +221,55 @@ def test_mlp_prefill_operands_bitwise(kq, m):
         assert np.all(np.isfinite(res[1])), name
         for i in range(m):
             assert_rms_close(res[1][i], want[i], what=f"mlp {name} row {i}")
+
+
+@pytest.mark.parametrize("m", [17, 24, 32, 33, 48, 63])
+def test_skinny_row_groups_bitwise(kq, m):
+    """The few-token kernel at 17 <= m <= 63 runs 32-row launches that multiply every unpacked weight
+    word with two 16-row groups of x (option 2, the default): the same bits as 16-row launches
+    (option 1) for the plain, accumulating, gate/up, QKV (with bias, and with the RMSNorm staged in
+    the kernel) and MLP (split K with the in-launch reduction) calls, and within the bar of the
+    oracle."""
+    s = synth()
+    lib = kq.lib()
+    case(f"few-token row groups m={m}: 32-row launches vs 16-row launches")
+    w = s.q4_weight(1000, 2048, 3101)
+    gw, uw = s.q4_weight(700, 1536, 3102), s.q4_weight(700, 1536, 3103)
+    qw, kw, vw = s.q4_weight(512, 1024, 3104), s.q4_weight(128, 1024, 3105), s.q4_weight(128, 1024, 3106)
+    mg, mu, md = s.q4_weight(4608, 512, 3107), s.q4_weight(4608, 512, 3108), s.q4_weight(512, 4608, 3109)
+    W, GW, UW, QW, KW, VW, MG, MU, MD = (q4_dev(kq, t) for t in (w, gw, uw, qw, kw, vw, mg, mu, md))
+    x = s.bf16_normal((m, 2048), 3110 + m)
+    xg = s.bf16_normal((m, 1536), 3111 + m)
+    xq = s.bf16_normal((m, 1024), 3112 + m)
+    xm = s.bf16_normal((m, 512), 3113 + m)
+    qb, kb, vb = (dev_bf16(s.bf16_normal((n,), 3114 + n)) for n in (512, 128, 128))
+    ln = dev_bf16(s.bf16_normal((1024,), 3115))
+    y0 = s.bf16_normal((m, 1000), 3116 + m)
+    res = {}
+    try:
+        for opt in (1, 2):
+            assert lib.kr_set_option(kq.OPT_SKINNY_GROUPS, opt) == 0
+            r = {}
+            r["linear"] = kq.q4_linear(W, dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy()
+            ya = dev_bf16(y0)
+            kq.q4_linear(W, dev_bf16(x), y=ya, accumulate=True)
+            r["accumulate"] = host_bits(ya)
+            r["gate_up"] = kq.gate_up_act(GW, UW, dev_bf16(xg), out_dtype=kq.DTYPE_F32).cpu().numpy()
+            r["qkv"] = [t.cpu().numpy() for t in kq.qkv(QW, KW, VW, dev_bf16(xq), qb, kb, vb)]
+            r["rmsnorm_qkv"] = [t.cpu().numpy() for t in kq.rmsnorm_qkv(dev_bf16(xq), ln, 1e-6, QW, KW, VW, qb, kb, vb)]
+            h = torch.zeros((m, 512), dtype=torch.float32, device="cuda")
+            kq.mlp(MG, MU, MD, h, x=dev_bf16(xm))
+            r["mlp"] = h.cpu().numpy()
+            res[opt] = r
+    finally:
+        lib.kr_set_option(kq.OPT_SKINNY_GROUPS, 2)
+    for name in res[1]:
+        a, b = res[1][name], res[2][name]
+        for u, v in zip(a if isinstance(a, list) else [a], b if isinstance(b, list) else [b]):
+            assert np.array_equal(np.ascontiguousarray(u).view(np.uint8), np.ascontiguousarray(v).view(np.uint8)), name
+    assert_rms_close(res[2]["linear"], O.q4_matmul(O.Q4Planar(*w), x), what=f"linear m={m}")
+    want_acc = O.bf16_to_f32(y0).astype(np.float64) + O.q4_matmul(O.Q4Planar(*w), x)
+    got_acc = O.bf16_to_f32(res[2]["accumulate"]).astype(np.float64)
+    assert np.all(np.abs(got_acc - want_acc) <= np.abs(want_acc) * 2.0 ** -8 + 1e-2 * rms(want_acc))
+    want_mlp = O.q4_mlp(O.Q4Planar(*mg), O.Q4Planar(*mu), O.Q4Planar(*md), xm)
+    assert_rms_close(res[2]["mlp"], want_mlp, what=f"mlp m={m}")
