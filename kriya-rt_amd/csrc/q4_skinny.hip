@@ -61,6 +61,20 @@ namespace {
 constexpr int kSkinnyWaves = 8;
 constexpr int kSkinnyPieces = 2;                                // 128-column pieces per wave
 constexpr int kSlabCols = kSkinnyWaves * kSkinnyPieces * 128;  // K columns per block
+#ifndef KR_SKINNY_DEPTH
+#define KR_SKINNY_DEPTH 2
+#endif
+constexpr int kSkinnyDepth = KR_SKINNY_DEPTH;  // dense mode: tiles whose words are in flight per wave
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
+template <class F, int... J>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, J...>) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 __device__ __forceinline__ uint32_t opq_s(uint32_t v) {
     uint32_t r;
@@ -86,6 +100,15 @@ __device__ __forceinline__ bf16x8_t q_frag(uint32_t w, uint32_t mask, uint32_t m
     return __builtin_bit_cast(bf16x8_t, r);
 }
 
+// The aligned 32-bit word holding the bf16 element at p, and that element (as f32) from the word.
+// (Pointer arithmetic, not an integer round trip, so that the load stays a global one.)
+__device__ __forceinline__ const uint32_t *word_of(const uint16_t *p) {
+    return reinterpret_cast<const uint32_t *>(p - ((reinterpret_cast<uintptr_t>(p) >> 1) & 1u));
+}
+__device__ __forceinline__ float half_f32(uint32_t word, const uint16_t *p) {
+    return __uint_as_float((reinterpret_cast<uintptr_t>(p) & 2) ? (word & 0xFFFF0000u) : (word << 16));
+}
+
 // XOR swizzle of row r's 16-byte units: the 16 rows of a fragment read hit distinct banks
 // (r & 15 alone measured 35-42 % bank-conflict cycles for these reads; this order, none).
 __device__ __forceinline__ uint32_t xs_swz(uint32_t r) { return ((r & 7u) << 1) | ((r >> 3) & 1u); }
@@ -105,11 +128,15 @@ __device__ __forceinline__ uint32_t xs_index(uint32_t r, uint32_t u) {
 // kGateUp: interleaved gate/up tiles with the activation epilogue;
 // kGrouped: MoE expert groups;
 // MG: groups of 16 token rows per launch (dense mode: 1 or 2).  With two, every unpacked weight
-// word is multiplied with both groups' X fragments (32 rows for the price of little more than 16).
-template <bool kGateUp, bool kGrouped, int MG>
+// word is multiplied with both groups' X fragments (32 rows for the price of little more than 16);
+// kPre: the epilogue reads a bias or the old output (dense mode, no split-K partials).  Launches
+// without either issue no such loads: the memory instructions per tile, not their bytes, set this
+// kernel's pace (measured: two dummy loads per tile cost 0.7 us of 13.8 at cfg1 B = 16 gate/up).
+template <bool kGateUp, bool kGrouped, int MG, bool kPre>
 __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_eu(kGrouped ? 4 : 2))) void q4_skinny_kernel(
     SkinnyArgs a) {
     static_assert(MG == 1 || (MG == 2 && !kGrouped), "two row groups in dense mode only");
+    static_assert(!(kPre && (kGrouped || kGateUp)), "bias and accumulation: dense plain tiles only");
     constexpr int NW = kSkinnyWaves;
     constexpr int KW = kSkinnyPieces;                  // 128-column pieces per wave
     constexpr uint32_t kTileRows = kGateUp ? 8 : 16;  // output features per tile
@@ -204,9 +231,14 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     // words in flight.
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
-    u32x4 wv[2][KW];
-    uint32_t sp[2][KW], bp[2][KW];
-    uint32_t pre_b[2] = {0, 0}, pre_o[2] = {0, 0};  // raw bits: converted at use, not at arrival
+    constexpr int D = kGrouped ? 2 : kSkinnyDepth;  // register buffers (tiles in flight + 1)
+    u32x4 wv[D][KW];
+    static_assert(KW == 2, "one scale/bias load per lane covers two pieces");
+    uint32_t sb[D];  // the lane's scale or bias word (see fetch_words)
+    // Raw 32-bit words, whose bf16 half is picked at use, not at arrival: a narrower value or a
+    // select at arrival has the compiler convert them at the loop's back edge, which then waits for
+    // the newest tile's operands and with them (loads complete in order) for the older tiles' words.
+    uint32_t pre_b[D] = {}, pre_o[D] = {};
     // epilogue output (token row erow, column ecol) of threads < 256 MG: row group tid / 256; the 64
     // threads of a wave read one v row of the reduction buffer (64 consecutive floats: no bank
     // conflicts)
@@ -214,23 +246,20 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
                    ecol = (uint32_t)tid & 15u;
     uint32_t orow = 0;                                                      // its output row (per segment)
     bool eout = false;                                                      // it stores an output
-    // The epilogue's operands of tile t: unconditional loads (threads without an operand read
-    // x[0]), so that no branch makes the compiler wait for them before its join.
+    // The epilogue's operands of tile t (dense mode; grouped launches have no bias and do not
+    // accumulate): unconditional loads (threads without an operand read x[0]), so that no branch
+    // makes the compiler wait for them before its join.  A bf16 element is read as the aligned
+    // 32-bit word holding it (such a word never crosses a page, so it is readable wherever the
+    // element is), and its half is picked at use.
     auto fetch_pre = [&](auto BUF, uint32_t e, uint32_t t) {
         constexpr int b = decltype(BUF)::value;
         const uint32_t ef = kGateUp ? t * 8 + (ecol & 7) : t * 16 + ecol;
         const bool ok = eout && ef < crows;
-        const uint16_t *bsrc = (cbias && ok) ? cbias + (size_t)e * crows + ef : a.x;
-        pre_b[b] = *bsrc;
-        // old output: an f32 or a bf16 load of exactly the element (both issued, from x when
-        // unused, so that no branch holds them up; a 32-bit read of a bf16 pair could pass the end)
+        pre_b[b] = *word_of((cbias && ok) ? cbias + (size_t)e * crows + ef : a.x);
         const size_t o = (size_t)orow * cldo + ef;
         const bool acc_ok = a.accumulate && ok;
-        const uint32_t *o32 = (acc_ok && a.out_f32) ? reinterpret_cast<const uint32_t *>(cout) + o
-                                                    : reinterpret_cast<const uint32_t *>(a.x);
-        const uint16_t *o16 = (acc_ok && !a.out_f32) ? reinterpret_cast<const uint16_t *>(cout) + o : a.x;
-        const uint32_t v32 = *o32, v16 = *o16;
-        pre_o[b] = a.out_f32 ? v32 : v16;
+        const uint16_t *osrc = reinterpret_cast<const uint16_t *>(cout) + (a.out_f32 ? 2 * o : o);
+        pre_o[b] = *word_of(acc_ok ? osrc : a.x);  // f32 outputs: their own (aligned) word
     };
     // The words (and scale/bias pairs) of tile t.
     auto fetch_words = [&](auto BUF, uint32_t e, uint32_t t) {
@@ -242,30 +271,29 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         f = f < crows ? f : crows - 1;  // tail rows re-read a valid row and are never stored
         const size_t row = (size_t)e * crows + f;
         const u32x4 *src = reinterpret_cast<const u32x4 *>(qw_base + row * kw + (k0 >> 3));
-        // bf16 pairs (groups 2p, 2p+1) of piece p; 4-byte aligned (kg even, scales 4-byte aligned)
-        const uint32_t *s32 = reinterpret_cast<const uint32_t *>(sc_base + row * kg + (k0 >> 6));
-        const uint32_t *b32 = reinterpret_cast<const uint32_t *>(bi_base + row * kg + (k0 >> 6));
 #pragma unroll
         for (int i = 0; i < KW; ++i) {
             uint32_t p = p0 + (uint32_t)i;
             p = p < npieces ? p : npieces - 1;
             wv[b][i] = ld_stream(src + 4 * p + g);
-            sp[b][i] = s32[p];
-            bp[b][i] = b32[p];
+        }
+        // The scales and biases of the wave's two pieces in one load: lane group g reads the bf16
+        // pair (groups 2p, 2p + 1) of piece p = p0 + (g >> 1), scales for even g, biases for odd g
+        // (4-byte aligned: kg even, scales and biases 4-byte aligned); tile_mma spreads them.
+        {
+            uint32_t p = p0 + ((uint32_t)g >> 1);
+            p = p < npieces ? p : npieces - 1;
+            const uint16_t *base = ((uint32_t)g & 1u) ? bi_base : sc_base;
+            sb[b] = reinterpret_cast<const uint32_t *>(base + row * kg + (k0 >> 6))[p];
         }
     };
-    // Dense mode requests the epilogue's operands first: loads complete in issue order, so a wait
-    // for them (an epilogue, or a register copy the compiler places at the loop's back edge) then
-    // does not also wait for the tile's words (measured: MLP at B = 16 27.5 -> 26.8 us).  Grouped
-    // mode keeps the words first (measured 2 % faster there).
+    // The epilogue's operands (when the launch has any) are requested first: loads complete in
+    // issue order, so a wait for them (an epilogue, or a register copy the compiler places at the
+    // loop's back edge) then does not also wait for the tile's words (measured: MLP at B = 16
+    // 27.5 -> 26.8 us).
     auto fetch = [&](auto BUF, uint32_t e, uint32_t t) {
-        if constexpr (kGrouped) {
-            fetch_words(BUF, e, t);
-            fetch_pre(BUF, e, t);
-        } else {
-            fetch_pre(BUF, e, t);
-            fetch_words(BUF, e, t);
-        }
+        if constexpr (kPre) fetch_pre(BUF, e, t);
+        fetch_words(BUF, e, t);
     };
 
     // X rows [base, base + rows) of the slab -> LDS (zeros beyond `rows` and
@@ -403,11 +431,16 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int gi = 0; gi < MG; ++gi) acc.v[gi] = f32x4{0, 0, 0, 0};
         const f32x4 zero = {0, 0, 0, 0};
+        // scale (even rows of lanes) and bias (odd rows) words, each then from lanes 0-31 (piece
+        // p0) and lanes 32-63 (piece p0 + 1) in every lane
+        const auto sbp = __builtin_amdgcn_permlane16_swap(sb[b], sb[b], false, false);
+        const auto spp = __builtin_amdgcn_permlane32_swap(sbp[0], sbp[0], false, false);
+        const auto bpp = __builtin_amdgcn_permlane32_swap(sbp[1], sbp[1], false, false);
 #pragma unroll
         for (int i = 0; i < KW; ++i) {
             // past the slab: the re-read words meet zero X; zero scales keep the products at 0
             const bool live = p0 + (uint32_t)i < npieces;
-            const uint32_t sv = live ? sp[b][i] : 0u, bv = live ? bp[b][i] : 0u;
+            const uint32_t sv = live ? spp[i] : 0u, bv = live ? bpp[i] : 0u;
             // swap words (0, 1) and (2, 3) across the lane halves: [0] holds group 2p, [1] group 2p + 1
             const auto p01 = __builtin_amdgcn_permlane32_swap(wv[b][i].x, wv[b][i].y, false, false);
             const auto p23 = __builtin_amdgcn_permlane32_swap(wv[b][i].z, wv[b][i].w, false, false);
@@ -474,14 +507,19 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
                     for (int w = 0; w < NW; ++w) up += red[par][eg][w][v][L + 8];
                     val = activation(val, a.act) * up;
                 }
-                if (cbias) val += bf16_to_f32(pre_b[b]);
                 const size_t o = (size_t)orow * cldo + f;
-                if (a.out_f32) {
-                    reinterpret_cast<float *>(cout)[o] = a.accumulate ? __uint_as_float(pre_o[b]) + val : val;
+                if constexpr (kPre) {
+                    if (cbias) val += half_f32(pre_b[b], cbias + f);
+                    if (a.out_f32) {
+                        reinterpret_cast<float *>(cout)[o] = a.accumulate ? __uint_as_float(pre_o[b]) + val : val;
+                    } else {
+                        uint16_t *dst = reinterpret_cast<uint16_t *>(cout) + o;
+                        *dst = (uint16_t)f32_to_bf16(a.accumulate ? val + half_f32(pre_o[b], dst) : val);
+                    }
+                } else if (a.out_f32) {
+                    reinterpret_cast<float *>(cout)[o] = val;
                 } else {
-                    const uint32_t old = pre_o[b] & 0xFFFFu;
-                    reinterpret_cast<uint16_t *>(cout)[o] =
-                        (uint16_t)f32_to_bf16(a.accumulate ? val + bf16_to_f32(old) : val);
+                    reinterpret_cast<uint16_t *>(cout)[o] = (uint16_t)f32_to_bf16(val);
                 }
             }
         }
@@ -491,7 +529,27 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     // each tile's successor is requested before it is multiplied.  The loop
     // body requests unconditionally and the last one or two tiles are peeled,
     // so that the compiler's wait counts never assume a skipped request.
+    // Deeper ring (dense mode, D > 2): tiles t + 1 .. t + D - 1 are in flight while tile t is
+    // multiplied; requests past the run's end re-request its last tile (same addresses: L2 hits,
+    // never stored), so that every request is unconditional.  prefetch_ring requests tiles
+    // t_begin + 1 .. t_begin + D - 2 (the caller requested t_begin into buffer 0).
+    auto prefetch_ring = [&](uint32_t e, uint32_t t_begin, uint32_t t_end) {
+        if constexpr (D > 2)
+            static_for<D - 2>([&](auto J) {
+                fetch(std::integral_constant<int, J + 1>{}, e, min(t_begin + (uint32_t)J + 1u, t_end - 1u));
+            });
+    };
     auto run_tiles = [&](uint32_t e, uint32_t t_begin, uint32_t t_end) {
+        if constexpr (D > 2) {
+            for (uint32_t t = t_begin; t < t_end; t += D) {
+                static_for<D>([&](auto J) {
+                    constexpr int j = J;
+                    fetch(std::integral_constant<int, (j + D - 1) % D>{}, e, min(t + (uint32_t)(j + D - 1), t_end - 1u));
+                    if (t + (uint32_t)j < t_end) finish(J, tile_mma(J), t + (uint32_t)j);
+                });
+            }
+            return;
+        }
         uint32_t t = t_begin;
         for (; t + 2 < t_end; t += 2) {
             fetch(B1{}, e, t + 1);
@@ -595,6 +653,12 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             crows = cw.n;
             return a.tile_begin[pi];
         };
+        // first tile of the problem after the one holding t (constant kernel-argument indices)
+        auto next_begin = [&](uint32_t t) -> uint32_t {
+            if (a.nmore > 0 && t < a.tile_begin[1]) return a.tile_begin[1];
+            if (a.nmore > 1 && t < a.tile_begin[2]) return a.tile_begin[2];
+            return a.nmore == 0 ? a.tile_begin[1] : a.nmore == 1 ? a.tile_begin[2] : a.tile_begin[3];
+        };
         uint32_t tb = select(run_begin);
         // X loads first (every row group's), then the first tile's words: the conversion waits for
         // X only.  The row groups pass through the one LDS slab in turn (the launcher gives a
@@ -603,6 +667,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         stage_load(raw[0], 0, rows0);
         if constexpr (MG == 2) stage_load(raw[MG - 1], 16, rows1);
         fetch(B0{}, 0, run_begin - tb);
+        prefetch_ring(0, run_begin - tb, min(run_end, next_begin(run_begin)) - tb);
         __builtin_amdgcn_sched_barrier(0);
         if (a.ln_w) norm_x(raw[0], rows0);
         stage_store(raw[0], rows0);
@@ -615,12 +680,6 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             lds_barrier();
             load_x_frags(std::integral_constant<int, MG - 1>{});
         }
-        // first tile of the problem after the one holding t (constant kernel-argument indices)
-        auto next_begin = [&](uint32_t t) -> uint32_t {
-            if (a.nmore > 0 && t < a.tile_begin[1]) return a.tile_begin[1];
-            if (a.nmore > 1 && t < a.tile_begin[2]) return a.tile_begin[2];
-            return a.nmore == 0 ? a.tile_begin[1] : a.nmore == 1 ? a.tile_begin[2] : a.tile_begin[3];
-        };
         uint32_t t = run_begin;
         for (;;) {
             const uint32_t seg_end = min(run_end, next_begin(t));
@@ -629,6 +688,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             if (t >= run_end) break;
             tb = select(t);
             fetch(B0{}, 0, t - tb);
+            prefetch_ring(0, t - tb, min(run_end, next_begin(t)) - tb);
         }
         if (a.tickets) reduce_run();
         return;
@@ -661,7 +721,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
 
 namespace {
 
-template <bool GU, bool G, int MG>
+template <bool GU, bool G, int MG, bool P>
 hipError_t launch_t(SkinnyArgs &a, uint32_t items, hipStream_t s) {
     // blocks per slab: every CU busy, each block a contiguous run of ceil(items / nblk) tiles
     // grouped (MoE) launches take twice the cap: cfg4 T = 64 is 1.3 % faster at 512 blocks, the dense
@@ -671,7 +731,7 @@ hipError_t launch_t(SkinnyArgs &a, uint32_t items, hipStream_t s) {
     if (a.tickets) cap = std::min(cap, kSkinnyTickets);  // one ticket word per run
     const uint32_t nblk = std::max<uint32_t>(1, std::min(items, cap));
     const dim3 grid(nblk * a.ksplit), block(kSkinnyWaves * 64);
-    hipLaunchKernelGGL((q4_skinny_kernel<GU, G, MG>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((q4_skinny_kernel<GU, G, MG, P>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 
@@ -687,7 +747,7 @@ hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s) {
     const bool grouped = a.offsets != nullptr;
     a.ksplit = skinny_ksplit(a.k);
     if (grouped && a.ksplit != 1) return hipErrorInvalidValue;
-    if (grouped && (a.nmore > 0 || a.ln_w)) return hipErrorInvalidValue;
+    if (grouped && (a.nmore > 0 || a.ln_w || a.bias || a.accumulate)) return hipErrorInvalidValue;
     if (a.nmore < 0 || a.nmore > 2 || (a.nmore > 0 && (gate_up || a.partial))) return hipErrorInvalidValue;
     if (!grouped && (a.m == 0 || a.m > kSkinnyMaxM)) return hipErrorInvalidValue;
     if (a.ln_w && a.ksplit != 1) return hipErrorInvalidValue;  // the norm needs the whole row in the slab
@@ -706,10 +766,20 @@ hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s) {
     }
     const uint32_t items =
         grouped ? a.max_active * ((a.expert_rows + tile_rows - 1) / tile_rows) : a.tile_begin[a.nmore + 1];
-    if (grouped) return gate_up ? launch_t<true, true, 1>(a, items, s) : launch_t<false, true, 1>(a, items, s);
-    if (a.m > 16)  // two row groups per launch
-        return gate_up ? launch_t<true, false, 2>(a, items, s) : launch_t<false, false, 2>(a, items, s);
-    return gate_up ? launch_t<true, false, 1>(a, items, s) : launch_t<false, false, 1>(a, items, s);
+    // the epilogue reads a bias or the old output (never with split-K partials: their reduction does)
+    bool pre = false;
+    if (!a.partial) {
+        pre = a.bias != nullptr || a.accumulate;
+        for (int i = 0; i < a.nmore; ++i) pre = pre || a.more[i].bias != nullptr;
+    }
+    if (grouped) return gate_up ? launch_t<true, true, 1, false>(a, items, s) : launch_t<false, true, 1, false>(a, items, s);
+    if (gate_up && pre) return hipErrorInvalidValue;  // gate/up launches have neither
+    if (a.m > 16) {  // two row groups per launch
+        if (gate_up) return launch_t<true, false, 2, false>(a, items, s);
+        return pre ? launch_t<false, false, 2, true>(a, items, s) : launch_t<false, false, 2, false>(a, items, s);
+    }
+    if (gate_up) return launch_t<true, false, 1, false>(a, items, s);
+    return pre ? launch_t<false, false, 1, true>(a, items, s) : launch_t<false, false, 1, false>(a, items, s);
 }
 
 uint32_t skinny_ksplit(uint32_t k) { return (k + kSlabCols - 1) / kSlabCols; }
