@@ -61,20 +61,6 @@ namespace {
 constexpr int kSkinnyWaves = 8;
 constexpr int kSkinnyPieces = 2;                                // 128-column pieces per wave
 constexpr int kSlabCols = kSkinnyWaves * kSkinnyPieces * 128;  // K columns per block
-#ifndef KR_SKINNY_DEPTH
-#define KR_SKINNY_DEPTH 2
-#endif
-constexpr int kSkinnyDepth = KR_SKINNY_DEPTH;  // dense mode: tiles whose words are in flight per wave
-
-// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
-template <class F, int... J>
-__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, J...>) {
-    (f(std::integral_constant<int, J>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
 
 __device__ __forceinline__ uint32_t opq_s(uint32_t v) {
     uint32_t r;
@@ -231,7 +217,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     // words in flight.
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
-    constexpr int D = kGrouped ? 2 : kSkinnyDepth;  // register buffers (tiles in flight + 1)
+    constexpr int D = 2;  // register buffers: the next tile is in flight while one is multiplied
     u32x4 wv[D][KW];
     static_assert(KW == 2, "one scale/bias load per lane covers two pieces");
     uint32_t sb[D];  // the lane's scale or bias word (see fetch_words)
@@ -529,27 +515,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     // each tile's successor is requested before it is multiplied.  The loop
     // body requests unconditionally and the last one or two tiles are peeled,
     // so that the compiler's wait counts never assume a skipped request.
-    // Deeper ring (dense mode, D > 2): tiles t + 1 .. t + D - 1 are in flight while tile t is
-    // multiplied; requests past the run's end re-request its last tile (same addresses: L2 hits,
-    // never stored), so that every request is unconditional.  prefetch_ring requests tiles
-    // t_begin + 1 .. t_begin + D - 2 (the caller requested t_begin into buffer 0).
-    auto prefetch_ring = [&](uint32_t e, uint32_t t_begin, uint32_t t_end) {
-        if constexpr (D > 2)
-            static_for<D - 2>([&](auto J) {
-                fetch(std::integral_constant<int, J + 1>{}, e, min(t_begin + (uint32_t)J + 1u, t_end - 1u));
-            });
-    };
     auto run_tiles = [&](uint32_t e, uint32_t t_begin, uint32_t t_end) {
-        if constexpr (D > 2) {
-            for (uint32_t t = t_begin; t < t_end; t += D) {
-                static_for<D>([&](auto J) {
-                    constexpr int j = J;
-                    fetch(std::integral_constant<int, (j + D - 1) % D>{}, e, min(t + (uint32_t)(j + D - 1), t_end - 1u));
-                    if (t + (uint32_t)j < t_end) finish(J, tile_mma(J), t + (uint32_t)j);
-                });
-            }
-            return;
-        }
         uint32_t t = t_begin;
         for (; t + 2 < t_end; t += 2) {
             fetch(B1{}, e, t + 1);
@@ -667,7 +633,6 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         stage_load(raw[0], 0, rows0);
         if constexpr (MG == 2) stage_load(raw[MG - 1], 16, rows1);
         fetch(B0{}, 0, run_begin - tb);
-        prefetch_ring(0, run_begin - tb, min(run_end, next_begin(run_begin)) - tb);
         __builtin_amdgcn_sched_barrier(0);
         if (a.ln_w) norm_x(raw[0], rows0);
         stage_store(raw[0], rows0);
@@ -688,7 +653,6 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             if (t >= run_end) break;
             tb = select(t);
             fetch(B0{}, 0, t - tb);
-            prefetch_ring(0, t - tb, min(run_end, next_begin(t)) - tb);
         }
         if (a.tickets) reduce_run();
         return;
