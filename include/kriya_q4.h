@@ -116,6 +116,10 @@ const char *kr_last_error(void);
 #define KR_OPT_SKINNY_GROUPS 15         /* few-token kernel, 17 <= m <= 63: 2 (default) 32-row launches, each
                                          * multiplying every unpacked weight word with two 16-row groups
                                          * of x; 1 16-row launches.  Bitwise the same results either way. */
+#define KR_OPT_SKINNY_DEPTH 16          /* few-token kernel, launches with no bias and no accumulation:
+                                         * 0 (default) three register buffers of tile words (two tiles
+                                         * in flight) when a block's run holds >= 6 tiles, else two;
+                                         * 2 or 3 forces that depth.  Bitwise the same results. */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 

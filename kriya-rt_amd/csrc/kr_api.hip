@@ -318,6 +318,10 @@ int kr_set_option(int option, int value) {
             if (value != 1 && value != 2) return fail(KR_E_INVALID, "few-token row groups must be 1 or 2");
             tuning().skinny_groups = value;
             return ok();
+        case KR_OPT_SKINNY_DEPTH:
+            if (value != 0 && value != 2 && value != 3) return fail(KR_E_INVALID, "few-token depth must be 0, 2 or 3");
+            tuning().skinny_depth = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -339,6 +343,7 @@ int kr_get_option(int option) {
         case KR_OPT_ATTN_MERGE_WAVE: return tuning().attn_merge_wave;
         case KR_OPT_PREFILL_OPERANDS: return tuning().prefill_operands;
         case KR_OPT_SKINNY_GROUPS: return tuning().skinny_groups;
+        case KR_OPT_SKINNY_DEPTH: return tuning().skinny_depth;
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }

@@ -44,6 +44,8 @@ struct Tuning {
                                        // 1 the barrier-free wave kernel, 0 the general block kernel
     int prefill_operands = 1;          // kr_q4_mlp at m >= 64: 1 fp16 operands converted once per call
     int skinny_groups = 2;             // dense few-token launches: 16-row groups per launch (1 or 2)
+    int skinny_depth = 0;              // dense few-token launches without epilogue operands: tiles
+                                       // in flight + 1; 0 = 3 for runs of >= 6 tiles, else 2
 };
 Tuning &tuning();
 

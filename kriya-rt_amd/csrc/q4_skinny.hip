@@ -62,6 +62,16 @@ constexpr int kSkinnyWaves = 8;
 constexpr int kSkinnyPieces = 2;                                // 128-column pieces per wave
 constexpr int kSlabCols = kSkinnyWaves * kSkinnyPieces * 128;  // K columns per block
 
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
+template <class F, int... J>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, J...>) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 __device__ __forceinline__ uint32_t opq_s(uint32_t v) {
     uint32_t r;
     asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
@@ -118,11 +128,14 @@ __device__ __forceinline__ uint32_t xs_index(uint32_t r, uint32_t u) {
 // kPre: the epilogue reads a bias or the old output (dense mode, no split-K partials).  Launches
 // without either issue no such loads: the memory instructions per tile, not their bytes, set this
 // kernel's pace (measured: two dummy loads per tile cost 0.7 us of 13.8 at cfg1 B = 16 gate/up).
-template <bool kGateUp, bool kGrouped, int MG, bool kPre>
+// D: register buffers of tile words, i.e. D - 1 tiles in flight while one is multiplied (2, or 3
+// for dense runs of at least 6 tiles: the launcher's choice).
+template <bool kGateUp, bool kGrouped, int MG, bool kPre, int D>
 __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_eu(kGrouped ? 4 : 2))) void q4_skinny_kernel(
     SkinnyArgs a) {
     static_assert(MG == 1 || (MG == 2 && !kGrouped), "two row groups in dense mode only");
     static_assert(!(kPre && (kGrouped || kGateUp)), "bias and accumulation: dense plain tiles only");
+    static_assert(D == 2 || (D == 3 && !kGrouped), "a deeper ring in dense mode only");
     constexpr int NW = kSkinnyWaves;
     constexpr int KW = kSkinnyPieces;                  // 128-column pieces per wave
     constexpr uint32_t kTileRows = kGateUp ? 8 : 16;  // output features per tile
@@ -217,7 +230,6 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     // words in flight.
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
-    constexpr int D = 2;  // register buffers: the next tile is in flight while one is multiplied
     u32x4 wv[D][KW];
     static_assert(KW == 2, "one scale/bias load per lane covers two pieces");
     uint32_t sb[D];  // the lane's scale or bias word (see fetch_words)
@@ -515,7 +527,31 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     // each tile's successor is requested before it is multiplied.  The loop
     // body requests unconditionally and the last one or two tiles are peeled,
     // so that the compiler's wait counts never assume a skipped request.
+    // Deeper ring (dense mode, D > 2): tiles t + 1 .. t + D - 1 are in flight while tile t is
+    // multiplied; tile t_begin + j lives in buffer j % D.  Requests past the run's end re-request
+    // its last tile (the same addresses: cache hits, never stored), so that every request is
+    // unconditional: a request under a branch leaves the compiler's wait counts conservative (it
+    // then waits for every tile in flight).  The launcher takes this ring for runs of at least
+    // 6 tiles, where such repeats are few (cfg1 gate/up at B = 16: 11.0 -> 9.9 us; at runs of 4
+    // tiles the repeats cost more than the depth gains).  prefetch_ring requests tiles
+    // t_begin + 1 .. t_begin + D - 2 (the caller requested t_begin into buffer 0).
+    auto prefetch_ring = [&](uint32_t e, uint32_t t_begin, uint32_t t_end) {
+        if constexpr (D > 2)
+            static_for<D - 2>([&](auto J) {
+                fetch(std::integral_constant<int, J + 1>{}, e, min(t_begin + (uint32_t)J + 1u, t_end - 1u));
+            });
+    };
     auto run_tiles = [&](uint32_t e, uint32_t t_begin, uint32_t t_end) {
+        if constexpr (D > 2) {
+            for (uint32_t t = t_begin; t < t_end; t += D) {
+                static_for<D>([&](auto J) {
+                    constexpr int j = J;
+                    fetch(std::integral_constant<int, (j + D - 1) % D>{}, e, min(t + (uint32_t)(j + D - 1), t_end - 1u));
+                    if (t + (uint32_t)j < t_end) finish(J, tile_mma(J), t + (uint32_t)j);
+                });
+            }
+            return;
+        }
         uint32_t t = t_begin;
         for (; t + 2 < t_end; t += 2) {
             fetch(B1{}, e, t + 1);
@@ -633,6 +669,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         stage_load(raw[0], 0, rows0);
         if constexpr (MG == 2) stage_load(raw[MG - 1], 16, rows1);
         fetch(B0{}, 0, run_begin - tb);
+        prefetch_ring(0, run_begin - tb, min(run_end, next_begin(run_begin)) - tb);
         __builtin_amdgcn_sched_barrier(0);
         if (a.ln_w) norm_x(raw[0], rows0);
         stage_store(raw[0], rows0);
@@ -653,6 +690,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             if (t >= run_end) break;
             tb = select(t);
             fetch(B0{}, 0, t - tb);
+            prefetch_ring(0, t - tb, min(run_end, next_begin(t)) - tb);
         }
         if (a.tickets) reduce_run();
         return;
@@ -685,6 +723,13 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
 
 namespace {
 
+template <bool GU, bool G, int MG, bool P, int D>
+hipError_t launch_d(SkinnyArgs &a, uint32_t nblk, hipStream_t s) {
+    const dim3 grid(nblk * a.ksplit), block(kSkinnyWaves * 64);
+    hipLaunchKernelGGL((q4_skinny_kernel<GU, G, MG, P, D>), grid, block, 0, s, a);
+    return hipGetLastError();
+}
+
 template <bool GU, bool G, int MG, bool P>
 hipError_t launch_t(SkinnyArgs &a, uint32_t items, hipStream_t s) {
     // blocks per slab: every CU busy, each block a contiguous run of ceil(items / nblk) tiles
@@ -694,9 +739,13 @@ hipError_t launch_t(SkinnyArgs &a, uint32_t items, hipStream_t s) {
     uint32_t cap = std::max<uint32_t>(1, cap_all / a.ksplit);
     if (a.tickets) cap = std::min(cap, kSkinnyTickets);  // one ticket word per run
     const uint32_t nblk = std::max<uint32_t>(1, std::min(items, cap));
-    const dim3 grid(nblk * a.ksplit), block(kSkinnyWaves * 64);
-    hipLaunchKernelGGL((q4_skinny_kernel<GU, G, MG, P>), grid, block, 0, s, a);
-    return hipGetLastError();
+    // the deeper ring for dense launches without epilogue operands whose runs hold >= 6 tiles
+    if constexpr (!G && !P) {
+        const int depth = tuning().skinny_depth;
+        const uint32_t per = (items + nblk - 1) / nblk;
+        if (depth == 3 || (depth == 0 && per >= 6)) return launch_d<GU, G, MG, P, 3>(a, nblk, s);
+    }
+    return launch_d<GU, G, MG, P, 2>(a, nblk, s);
 }
 
 }  // namespace

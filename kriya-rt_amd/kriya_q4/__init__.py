@@ -37,6 +37,7 @@ OPT_SPLITK_TICKETS = 12
 OPT_ATTN_MERGE_WAVE = 13
 OPT_PREFILL_OPERANDS = 14
 OPT_SKINNY_GROUPS = 15
+OPT_SKINNY_DEPTH = 16
 
 _lib = None
 

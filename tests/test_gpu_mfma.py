@@ -273,3 +273,43 @@ def test_skinny_row_groups_bitwise(kq, m):
     assert np.all(np.abs(got_acc - want_acc) <= np.abs(want_acc) * 2.0 ** -8 + 1e-2 * rms(want_acc))
     want_mlp = O.q4_mlp(O.Q4Planar(*mg), O.Q4Planar(*mu), O.Q4Planar(*md), xm)
     assert_rms_close(res[2]["mlp"], want_mlp, what=f"mlp m={m}")
+
+
+@pytest.mark.parametrize("m", [5, 16, 24])
+def test_skinny_depth_bitwise(kq, m):
+    """The few-token kernel's register ring (two tiles in flight, chosen for runs of >= 6 tiles, or
+    forced with KR_OPT_SKINNY_DEPTH) gives the same bits as one tile in flight: gate/up and plain
+    launches whose runs hold 1..6 tiles with ragged ends, one and two row groups, and the MLP (its
+    split-K down projection reduces inside the launch); the default against the oracle too."""
+    s = synth()
+    lib = kq.lib()
+    case(f"few-token ring depth m={m}: depth 2 vs 3 vs automatic")
+    shapes = [(11008, 2048), (10995, 2048), (300, 1024), (3000, 1536)]
+    mats = [(s.q4_weight(n, k, 3201 + i), s.q4_weight(n, k, 3301 + i)) for i, (n, k) in enumerate(shapes)]
+    dev = [(q4_dev(kq, g), q4_dev(kq, u)) for g, u in mats]
+    xs = [s.bf16_normal((m, k), 3401 + i + m) for i, (_, k) in enumerate(shapes)]
+    mg, mu, md = s.q4_weight(4608, 512, 3501), s.q4_weight(4608, 512, 3502), s.q4_weight(512, 4608, 3503)
+    MG, MU, MD = (q4_dev(kq, t) for t in (mg, mu, md))
+    xm = s.bf16_normal((m, 512), 3504 + m)
+    res = {}
+    try:
+        for opt in (2, 3, 0):
+            assert lib.kr_set_option(kq.OPT_SKINNY_DEPTH, opt) == 0
+            r = []
+            for (G, U), x in zip(dev, xs):
+                r.append(kq.gate_up_act(G, U, dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy())
+                r.append(host_bits(kq.gate_up_act(G, U, dev_bf16(x), out_dtype=kq.DTYPE_BF16)))
+                r.append(kq.q4_linear(G, dev_bf16(x), out_dtype=kq.DTYPE_F32).cpu().numpy())
+            h = torch.zeros((m, 512), dtype=torch.float32, device="cuda")
+            kq.mlp(MG, MU, MD, h, x=dev_bf16(xm))
+            r.append(h.cpu().numpy())
+            res[opt] = r
+    finally:
+        lib.kr_set_option(kq.OPT_SKINNY_DEPTH, 0)
+    for opt in (3, 0):
+        for i, (a, b) in enumerate(zip(res[2], res[opt])):
+            assert np.array_equal(np.ascontiguousarray(a).view(np.uint8), np.ascontiguousarray(b).view(np.uint8)), (opt, i)
+    for i, ((g, u), x) in enumerate(zip(mats, xs)):
+        assert_rms_close(res[0][3 * i], O.q4_gate_up_act(O.Q4Planar(*g), O.Q4Planar(*u), x), what=f"gate/up {shapes[i]}")
+        assert_rms_close(res[0][3 * i + 2], O.q4_matmul(O.Q4Planar(*g), x), what=f"linear {shapes[i]}")
+    assert_rms_close(res[0][-1], O.q4_mlp(O.Q4Planar(*mg), O.Q4Planar(*mu), O.Q4Planar(*md), xm), what="mlp")
