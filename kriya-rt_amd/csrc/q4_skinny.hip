@@ -598,33 +598,86 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         const uint32_t f0 = run_begin * kTileRows, f1 = min(run_end * kTileRows, n);
         const uint32_t nrows = f1 - f0, items = nrows * a.m;
         const size_t stride = (size_t)a.m * nw * n;
-        for (uint32_t it = (uint32_t)tid; it < items; it += NW * 64) {
-            const uint32_t tok = it / nrows, f = f0 + it % nrows;
+        // Four consecutive features per thread (16-byte loads of every slab's partials and one
+        // load of the old outputs, all issued before any store: one round trip) when the run's
+        // features and the rows stay 16-byte aligned; else one feature per thread.
+        const bool vec = nrows % 4 == 0 && n % 4 == 0 && a.ldo % 4 == 0 && (uintptr_t)a.partial % 16 == 0 &&
+                         (uintptr_t)a.out % 16 == 0 && !a.bias && (size_t)a.ksplit * stride * 4 < (1ull << 31);
+        const uint32_t width = vec ? 4u : 1u, vitems = items / width, vrows = nrows / width;
+        for (uint32_t it = (uint32_t)tid; it < vitems; it += NW * 64) {
+            const uint32_t tok = it / vrows, f = f0 + (it % vrows) * width;
             const float *p = a.partial + (size_t)tok * nw * n + f;
-            float gs[kSkinnyMaxTicketSplit], us[kSkinnyMaxTicketSplit];
+            const size_t o = (size_t)tok * a.ldo + f;
+            f32x4 gsum = {0, 0, 0, 0}, usum = {0, 0, 0, 0}, old = {0, 0, 0, 0};
+            if (vec) {
+                // device-coherent 16-byte loads (the sc1 policy of the scalar path's agent-scope atomic
+                // loads: never served from a stale line of this XCD's L2), through a buffer resource
+                // over the partials; offsets below 2^32 bytes (the launcher checks)
+                const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+                    a.partial, (short)0, (int)((size_t)a.ksplit * stride * 4), 0x00020000);
+                const uint32_t pb = (uint32_t)((size_t)tok * nw * n + f) * 4u;
+                f32x4 gs[kSkinnyMaxTicketSplit], us[kSkinnyMaxTicketSplit];
 #pragma unroll
-            for (uint32_t sl = 0; sl < kSkinnyMaxTicketSplit; ++sl) {  // unconditional (clamped) loads
-                const size_t off = (size_t)min(sl, a.ksplit - 1) * stride;
-                gs[sl] = __hip_atomic_load(p + off, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                us[sl] = nw == 2 ? __hip_atomic_load(p + off + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
-            }
-            float gsum = 0.0f, usum = 0.0f;
+                for (uint32_t sl = 0; sl < kSkinnyMaxTicketSplit; ++sl) {  // unconditional (clamped) loads
+                    const uint32_t off = pb + (uint32_t)(min(sl, a.ksplit - 1) * stride) * 4u;
+                    gs[sl] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, 16));
+                    if (nw == 2) us[sl] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, off + n * 4u, 0, 16));
+                }
+                if (a.accumulate) {
+                    if (a.out_f32) {
+                        old = *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(a.out) + o);
+                    } else {
+                        const uint2 ob = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(a.out) + o);
+                        old = f32x4{__uint_as_float(ob.x << 16), __uint_as_float(ob.x & 0xFFFF0000u),
+                                    __uint_as_float(ob.y << 16), __uint_as_float(ob.y & 0xFFFF0000u)};
+                    }
+                }
 #pragma unroll
-            for (uint32_t sl = 0; sl < kSkinnyMaxTicketSplit; ++sl) {
-                if (sl < a.ksplit) {
-                    gsum += gs[sl];
-                    usum += us[sl];
+                for (uint32_t sl = 0; sl < kSkinnyMaxTicketSplit; ++sl) {
+                    if (sl < a.ksplit) {
+                        gsum += gs[sl];
+                        if (nw == 2) usum += us[sl];
+                    }
+                }
+            } else {
+                float gs[kSkinnyMaxTicketSplit], us[kSkinnyMaxTicketSplit];
+#pragma unroll
+                for (uint32_t sl = 0; sl < kSkinnyMaxTicketSplit; ++sl) {
+                    const size_t off = (size_t)min(sl, a.ksplit - 1) * stride;
+                    gs[sl] = __hip_atomic_load(p + off, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    us[sl] = nw == 2 ? __hip_atomic_load(p + off + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+                }
+                if (a.accumulate)
+                    old[0] = a.out_f32 ? reinterpret_cast<const float *>(a.out)[o]
+                                       : bf16_to_f32(reinterpret_cast<const uint16_t *>(a.out)[o]);
+#pragma unroll
+                for (uint32_t sl = 0; sl < kSkinnyMaxTicketSplit; ++sl) {
+                    if (sl < a.ksplit) {
+                        gsum[0] += gs[sl];
+                        usum[0] += us[sl];
+                    }
                 }
             }
-            float val = kGateUp ? activation(gsum, a.act) * usum : gsum;
-            if (a.bias) val += bf16_to_f32(a.bias[f]);
-            const size_t o = (size_t)tok * a.ldo + f;
+            float val[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                val[e] = kGateUp ? activation(gsum[e], a.act) * usum[e] : gsum[e];
+                if (a.bias) val[e] += bf16_to_f32(a.bias[f + e]);  // (scalar path only)
+                if (a.accumulate) val[e] = a.out_f32 ? old[e] + val[e] : val[e] + old[e];
+            }
             if (a.out_f32) {
-                float *out = reinterpret_cast<float *>(a.out);
-                out[o] = a.accumulate ? out[o] + val : val;
+                float *out = reinterpret_cast<float *>(a.out) + o;
+                if (vec)
+                    *reinterpret_cast<f32x4 *>(out) = f32x4{val[0], val[1], val[2], val[3]};
+                else
+                    out[0] = val[0];
             } else {
-                uint16_t *out = reinterpret_cast<uint16_t *>(a.out);
-                out[o] = (uint16_t)f32_to_bf16(a.accumulate ? val + bf16_to_f32(out[o]) : val);
+                uint16_t *out = reinterpret_cast<uint16_t *>(a.out) + o;
+                if (vec)
+                    *reinterpret_cast<uint2 *>(out) = uint2{f32_to_bf16(val[0]) | (f32_to_bf16(val[1]) << 16),
+                                                            f32_to_bf16(val[2]) | (f32_to_bf16(val[3]) << 16)};
+                else
+                    out[0] = (uint16_t)f32_to_bf16(val[0]);
             }
         }
         if (tid == 0) __hip_atomic_store(&a.tickets[rb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
