@@ -96,15 +96,6 @@ __device__ __forceinline__ bf16x8_t q_frag(uint32_t w, uint32_t mask, uint32_t m
     return __builtin_bit_cast(bf16x8_t, r);
 }
 
-// The aligned 32-bit word holding the bf16 element at p, and that element (as f32) from the word.
-// (Pointer arithmetic, not an integer round trip, so that the load stays a global one.)
-__device__ __forceinline__ const uint32_t *word_of(const uint16_t *p) {
-    return reinterpret_cast<const uint32_t *>(p - ((reinterpret_cast<uintptr_t>(p) >> 1) & 1u));
-}
-__device__ __forceinline__ float half_f32(uint32_t word, const uint16_t *p) {
-    return __uint_as_float((reinterpret_cast<uintptr_t>(p) & 2) ? (word & 0xFFFF0000u) : (word << 16));
-}
-
 // XOR swizzle of row r's 16-byte units: the 16 rows of a fragment read hit distinct banks
 // (r & 15 alone measured 35-42 % bank-conflict cycles for these reads; this order, none).
 __device__ __forceinline__ uint32_t xs_swz(uint32_t r) { return ((r & 7u) << 1) | ((r >> 3) & 1u); }
@@ -136,6 +127,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     static_assert(MG == 1 || (MG == 2 && !kGrouped), "two row groups in dense mode only");
     static_assert(!(kPre && (kGrouped || kGateUp)), "bias and accumulation: dense plain tiles only");
     static_assert(D == 2 || (D == 3 && !kGrouped), "a deeper ring in dense mode only");
+    static_assert(!kPre || D == 2, "epilogue operands with one tile in flight only");
     constexpr int NW = kSkinnyWaves;
     constexpr int KW = kSkinnyPieces;                  // 128-column pieces per wave
     constexpr uint32_t kTileRows = kGateUp ? 8 : 16;  // output features per tile
@@ -233,9 +225,8 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     u32x4 wv[D][KW];
     static_assert(KW == 2, "one scale/bias load per lane covers two pieces");
     uint32_t sb[D];  // the lane's scale or bias word (see fetch_words)
-    // Raw 32-bit words, whose bf16 half is picked at use, not at arrival: a narrower value or a
-    // select at arrival has the compiler convert them at the loop's back edge, which then waits for
-    // the newest tile's operands and with them (loads complete in order) for the older tiles' words.
+    // The epilogue's operands as raw bits (a bf16 in the low half, or an f32), converted at use.
+    // Only launches with one tile in flight have them (kPre implies D = 2).
     uint32_t pre_b[D] = {}, pre_o[D] = {};
     // epilogue output (token row erow, column ecol) of threads < 256 MG: row group tid / 256; the 64
     // threads of a wave read one v row of the reduction buffer (64 consecutive floats: no bank
@@ -245,19 +236,21 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     uint32_t orow = 0;                                                      // its output row (per segment)
     bool eout = false;                                                      // it stores an output
     // The epilogue's operands of tile t (dense mode; grouped launches have no bias and do not
-    // accumulate): unconditional loads (threads without an operand read x[0]), so that no branch
-    // makes the compiler wait for them before its join.  A bf16 element is read as the aligned
-    // 32-bit word holding it (such a word never crosses a page, so it is readable wherever the
-    // element is), and its half is picked at use.
+    // accumulate): loads of exactly the element, unconditional (threads without an operand read
+    // x[0], or the first weight word for an f32), so that no branch on the thread makes the
+    // compiler wait for them before its join.  The old output is an f32 or a bf16 load under a
+    // launch-uniform branch, one load either way.
     auto fetch_pre = [&](auto BUF, uint32_t e, uint32_t t) {
         constexpr int b = decltype(BUF)::value;
         const uint32_t ef = kGateUp ? t * 8 + (ecol & 7) : t * 16 + ecol;
         const bool ok = eout && ef < crows;
-        pre_b[b] = *word_of((cbias && ok) ? cbias + (size_t)e * crows + ef : a.x);
+        pre_b[b] = *((cbias && ok) ? cbias + (size_t)e * crows + ef : a.x);
         const size_t o = (size_t)orow * cldo + ef;
         const bool acc_ok = a.accumulate && ok;
-        const uint16_t *osrc = reinterpret_cast<const uint16_t *>(cout) + (a.out_f32 ? 2 * o : o);
-        pre_o[b] = *word_of(acc_ok ? osrc : a.x);  // f32 outputs: their own (aligned) word
+        if (a.out_f32)
+            pre_o[b] = *(acc_ok ? reinterpret_cast<const uint32_t *>(cout) + o : cw.qw);
+        else
+            pre_o[b] = *(acc_ok ? reinterpret_cast<const uint16_t *>(cout) + o : a.x);
     };
     // The words (and scale/bias pairs) of tile t.
     auto fetch_words = [&](auto BUF, uint32_t e, uint32_t t) {
@@ -507,12 +500,12 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
                 }
                 const size_t o = (size_t)orow * cldo + f;
                 if constexpr (kPre) {
-                    if (cbias) val += half_f32(pre_b[b], cbias + f);
+                    if (cbias) val += __uint_as_float(pre_b[b] << 16);
                     if (a.out_f32) {
                         reinterpret_cast<float *>(cout)[o] = a.accumulate ? __uint_as_float(pre_o[b]) + val : val;
                     } else {
                         uint16_t *dst = reinterpret_cast<uint16_t *>(cout) + o;
-                        *dst = (uint16_t)f32_to_bf16(a.accumulate ? val + half_f32(pre_o[b], dst) : val);
+                        *dst = (uint16_t)f32_to_bf16(a.accumulate ? val + __uint_as_float(pre_o[b] << 16) : val);
                     }
                 } else if (a.out_f32) {
                     reinterpret_cast<float *>(cout)[o] = val;
