@@ -438,6 +438,14 @@ int kr_q4_linear(const kr_q4_matrix *w, const uint16_t *x, uint32_t m, void *y, 
     return hip_status(launch_mfma(args, bm_class(m), s), "kr_q4_linear");
 }
 
+// Gate/up at 2 <= m <= 4 on the token GEMV kernel, except at m = 4 where the few-token matrix-core
+// kernel is faster when it fits (cfg1 shape: 9.7 against 11.3 us; m = 3: 9.7 both, m = 2: 8.4
+// against 9.7).  The down projection keeps the token GEMV at m <= 4 (cfg1 m = 4: 9.0 against 10.8).
+static bool gate_up_on_tokens(uint32_t m, const Q4Mat &g, const Q4Mat &u) {
+    if (!(tuning().gemv_tokens && gemv_tokens_supported(m, g.k, true))) return false;
+    return m <= 3 || !(skinny_fits(m, g, false) && skinny_supported(u));
+}
+
 int kr_q4_gate_up_act(const kr_q4_matrix *gate, const kr_q4_matrix *up, const uint16_t *x, uint32_t m,
                       void *act_out, int act_dtype, int activation, void *stream) {
     if (int rc = check_matrix(gate, "gate")) return rc;
@@ -456,7 +464,7 @@ int kr_q4_gate_up_act(const kr_q4_matrix *gate, const kr_q4_matrix *up, const ui
         const int epi = act_dtype == KR_DTYPE_F32 ? kGateUpF32 : kGateUpBF16;
         return hip_status(launch_gemv(g, &u, x, act_out, epi, activation, nullptr, s), "kr_q4_gate_up_act");
     }
-    if (tuning().gemv_tokens && gemv_tokens_supported(m, gate->k, true)) {
+    if (gate_up_on_tokens(m, g, u)) {
         const int epi = act_dtype == KR_DTYPE_F32 ? kGateUpF32 : kGateUpBF16;
         return hip_status(launch_gemv_tokens(g, &u, x, m, act_out, gate->n, epi, activation, nullptr, s),
                           "kr_q4_gate_up_act");
@@ -963,7 +971,7 @@ int kr_rmsnorm_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
             return rc;
         return kr_q4_linear(down, act, 1, h, KR_DTYPE_BF16, 1, stream);
     }
-    const bool tokens = tuning().gemv_tokens && gemv_tokens_supported(m, gate->k, true);
+    const bool tokens = gate_up_on_tokens(m, to_mat(gate), to_mat(up));
     if (!tokens && skinny_fits(m, to_mat(gate), false) && skinny_supported(to_mat(up))) {
         // few tokens on the matrix cores: the norm is applied while gate/up stages x
         uint16_t *act = mlp_ws_act(workspace);
