@@ -86,27 +86,98 @@ __device__ __forceinline__ float activation(float g, int variant) {
     return fmaxf(g, 0.0f);
 }
 
-// ---- wavefront reductions (64 lanes)
-// Reduces R per-lane values at once.  The first log2(R) butterfly steps swap
-// halves of the value set between lane pairs, so each step moves R/2, R/4, ...
-// values instead of R; afterwards every lane of the 64/R-lane segment s holds
+// ---- wavefront reductions (64 lanes), without LDS
+// One fixed pairing tree over the 64 lanes, level by level: lane l ^ 32 (v_permlane32_swap),
+// l ^ 16 (v_permlane16_swap), l ^ 8 (DPP row_ror:8), the mirror lane of its group of 8 (DPP
+// row_half_mirror), l ^ 2 and l ^ 1 (DPP quad_perm).  A reduction of R values first halves the
+// value set at the top levels (each lane keeps the half it owns and adds its partner's copy of
+// it), so that segment s of 64 / R lanes ends with value s; the remaining levels sum within
+// the segment.  Every value is summed over the same tree whatever R is, and all lanes of a
+// segment hold the same bits.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+// partner's copy of v at tree level L (0: l ^ 32 ... 5: l ^ 1); whether lane is the pair's upper
+template <int L>
+__device__ __forceinline__ float tree_partner(float v, int lane) {
+    if constexpr (L == 0) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(lane < 32 ? p[1] : p[0]);
+    } else if constexpr (L == 1) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float((lane & 16) ? p[0] : p[1]);
+    } else if constexpr (L == 2) {
+        return dpp_f32<0x128>(v);  // row_ror:8, i.e. lane ^ 8 within the 16-lane row
+    } else if constexpr (L == 3) {
+        return dpp_f32<0x141>(v);  // row_half_mirror: lane 7 - i of its group of 8
+    } else if constexpr (L == 4) {
+        return dpp_f32<0x4E>(v);  // quad_perm [2, 3, 0, 1]
+    } else {
+        return dpp_f32<0xB1>(v);  // quad_perm [1, 0, 3, 2]
+    }
+}
+template <int L>
+__device__ __forceinline__ bool tree_upper(int lane) {
+    return (lane & (32 >> L)) != 0;  // (level 3: lanes 4..7 of each group of 8)
+}
+// One halving level over values v[i] (i < half) and v[i + half]: the lower lane of each pair
+// keeps value i, the upper value i + half, each plus its partner's copy.
+template <int L, int kHalf, class V>
+__device__ __forceinline__ void tree_halve(V &v, int lane) {
+    constexpr int half = kHalf;
+    if constexpr (L <= 1) {  // one swap instruction exchanges both values of the pair
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            const uint32_t a = __float_as_uint(v[i]), b = __float_as_uint(v[i + half]);
+            if constexpr (L == 0) {
+                const auto p = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+                v[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+            } else {
+                const auto p = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+                v[i] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+            }
+        }
+    } else {
+        // both values summed with their partner copies, then the lane's one picked: a select
+        // between the two vector elements instead is turned into a run-time element index,
+        // which the back end expands into a compare-and-select over the whole vector
+        const bool upper = tree_upper<L>(lane);
+#pragma unroll
+        for (int i = 0; i < half; ++i) {
+            const float lo = v[i] + tree_partner<L>(v[i], lane);
+            const float hi = v[i + half] + tree_partner<L>(v[i + half], lane);
+            v[i] = upper ? hi : lo;
+        }
+    }
+}
+template <int L>
+__device__ __forceinline__ float tree_sum_from(float s, int lane) {
+    if constexpr (L <= 5) {
+        s += tree_partner<L>(s, lane);
+        return tree_sum_from<L + 1>(s, lane);
+    } else {
+        return s;
+    }
+}
+template <int N, class V>
+__device__ __forceinline__ float tree_reduce(V &v, int lane) {
+    static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "a power of two of values");
+    if constexpr (N >= 2) tree_halve<0, N / 2>(v, lane);
+    if constexpr (N >= 4) tree_halve<1, N / 4>(v, lane);
+    if constexpr (N >= 8) tree_halve<2, N / 8>(v, lane);
+    if constexpr (N >= 16) tree_halve<3, N / 16>(v, lane);
+    if constexpr (N >= 32) tree_halve<4, N / 32>(v, lane);
+    if constexpr (N >= 64) tree_halve<5, N / 64>(v, lane);
+    constexpr int kLevels = N == 1 ? 0 : N == 2 ? 1 : N == 4 ? 2 : N == 8 ? 3 : N == 16 ? 4 : N == 32 ? 5 : 6;
+    return tree_sum_from<kLevels>(v[0], lane);
+}
+
+// Reduces R per-lane values at once; afterwards every lane of the 64 / R-lane segment s holds
 // the total of value s.  Fixed order: the result is identical on every launch.
 template <int R>
 __device__ __forceinline__ float wave_reduce_rows(float (&v)[R], int lane) {
-#pragma unroll
-    for (int half = R / 2, mask = 32; half >= 1; half >>= 1, mask >>= 1) {
-        const bool upper = (lane & mask) != 0;
-#pragma unroll
-        for (int i = 0; i < half; ++i) {
-            float send = upper ? v[i] : v[i + half];
-            float keep = upper ? v[i + half] : v[i];
-            v[i] = keep + __shfl_xor(send, mask);
-        }
-    }
-    float s = v[0];
-#pragma unroll
-    for (int mask = 32 / R; mask >= 1; mask >>= 1) s += __shfl_xor(s, mask);
-    return s;
+    return tree_reduce<R>(v, lane);
 }
 
 // The same over a vector of N values (an SSA value: a float array here was
@@ -118,22 +189,12 @@ struct FVec {
 };
 template <int N>
 __device__ __forceinline__ float wave_reduce_vec(typename FVec<N>::type v, int lane) {
-#pragma unroll
-    for (int half = N / 2, mask = 32; half >= 1; half >>= 1, mask >>= 1) {
-        const bool upper = (lane & mask) != 0;
-#pragma unroll
-        for (int i = 0; i < half; ++i) {
-            const float lo = v[i], hi = v[i + half];
-            const float send = upper ? lo : hi;
-            const float keep = upper ? hi : lo;
-            v[i] = keep + __shfl_xor(send, mask);
-        }
-    }
-    float s = v[0];
-#pragma unroll
-    for (int mask = 32 / N; mask >= 1; mask >>= 1) s += __shfl_xor(s, mask);
-    return s;
+    return tree_reduce<N>(v, lane);
 }
+
+// The value of lane l ^ 32 or l ^ 16 (one swap instruction, no LDS).
+__device__ __forceinline__ float xchg32(float v, int lane) { return tree_partner<0>(v, lane); }
+__device__ __forceinline__ float xchg16(float v, int lane) { return tree_partner<1>(v, lane); }
 
 // ---- activations outside fp16's range on the fp16 matrix-core paths.
 // fp16 holds a bf16 value exactly only within [2^-14, 65504]: a token row whose

@@ -195,7 +195,8 @@ __device__ __forceinline__ void tile_epilogue(float tot, int lane, uint32_t t, u
     const uint32_t r = v / MP, tok = v % MP;
     if (tok >= (uint32_t)M) return;
     if (kGateUp) {
-        const float up = __shfl_xor(tot, kWave / R);  // row r + 1 of the same token
+        // row r + 1 of the same token, from the lane that holds it
+        const float up = kWave / R == 32 ? xchg32(tot, lane) : kWave / R == 16 ? xchg16(tot, lane) : __shfl_xor(tot, kWave / R);
         if ((lane % kSeg) == 0 && (r & 1) == 0) {
             const uint32_t ch = t * (R / 2) + (r >> 1);
             if (ch < nrows) store_row<EPI>(o, tok * o.ldo + ch, activation(tot, o.act) * up, 0.0f);
