@@ -192,6 +192,9 @@ __device__ __forceinline__ float wave_reduce_vec(typename FVec<N>::type v, int l
     return tree_reduce<N>(v, lane);
 }
 
+// Sum over all 64 lanes on the same tree, every lane holding the same bits (no LDS).
+__device__ __forceinline__ float wave_total(float v, int lane) { return tree_sum_from<0>(v, lane); }
+
 // The value of lane l ^ 32 or l ^ 16 (one swap instruction, no LDS).
 __device__ __forceinline__ float xchg32(float v, int lane) { return tree_partner<0>(v, lane); }
 __device__ __forceinline__ float xchg16(float v, int lane) { return tree_partner<1>(v, lane); }

@@ -376,7 +376,7 @@ __device__ __forceinline__ void gemv_wave_loop(const GemvBatch &gb, const uint16
                     }
                 }
             }
-            ss = wave_sum(ss);
+            ss = wave_total(ss, lane);
             if (lane == 0) s_ss[tid >> 6] = ss;
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // LDS only: the words stay in flight
             const float scale = 1.0f / sqrtf((((s_ss[0] + s_ss[1]) + s_ss[2]) + s_ss[3]) / (float)K + gb.eps);

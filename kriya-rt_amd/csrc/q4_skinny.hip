@@ -345,7 +345,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
                     ss = fmaf(hi, hi, ss);
                 }
             }
-            ss = wave_sum(ss);
+            ss = wave_total(ss, lane);
             if (lane == 0) s_ss[r][wave & 3] = ss;
         }
         lds_barrier();
