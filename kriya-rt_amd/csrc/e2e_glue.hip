@@ -186,8 +186,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_decode_kernel(
         sc[p] = dot;
         mx = fmaxf(mx, dot);
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+    mx = wave_max(mx);
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
     mx = red[0];
@@ -449,12 +448,10 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
         const float dot = ((sp[0][r][c] + sp[1][r][c]) + sp[2][r][c]) + sp[3][r][c];
         const float x = p0 + c < p1 ? dot * (1.0f / sqrtf((float)D)) : -INFINITY;
         float m = x;
-#pragma unroll
-        for (int sh = 8; sh >= 1; sh >>= 1) m = fmaxf(m, __shfl_xor(m, sh));
+        m = tree_max_from<2>(m, (int)__lane_id());  // over the row's 16 lanes
         const float e = x == -INFINITY ? 0.0f : expf(x - m);
         float l = e;
-#pragma unroll
-        for (int sh = 8; sh >= 1; sh >>= 1) l += __shfl_xor(l, sh);
+        l = tree_sum_from<2>(l, (int)__lane_id());
         sc[r][c] = e;
         m_keep = m;
         l_keep = l;
@@ -514,8 +511,7 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
 // sum_s w_s l_s are block reductions in a fixed order; the value sums run in slice order per
 // interleave, interleaves added in order; earlier rounds are rescaled to the new max.
 __device__ __forceinline__ float block_max256(float v, float *red) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    v = wave_max(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
     v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -615,8 +611,7 @@ __global__ __launch_bounds__(256) void attention_combine_wave_kernel(const float
     for (uint32_t j = 0; j < J; ++j) a[j] = base[min(il + NI * j, splits - 1) * stride + 2 * G + g * D + d];
     const float mt = lane < splits ? mraw : -INFINITY;
     float M = mt;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
+    M = wave_max(M);
     const float wt = mt == -INFINITY ? 0.0f : expf(mt - M);
     const float L = wave_sum(wt * (lane < splits ? lraw : 0.0f));
     sw[w][lane] = wt;

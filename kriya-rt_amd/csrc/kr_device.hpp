@@ -194,6 +194,17 @@ __device__ __forceinline__ float wave_reduce_vec(typename FVec<N>::type v, int l
 
 // Sum over all 64 lanes on the same tree, every lane holding the same bits (no LDS).
 __device__ __forceinline__ float wave_total(float v, int lane) { return tree_sum_from<0>(v, lane); }
+// Max over the lanes from tree level L0 on (0: all 64, 2: each row of 16); max is exact, so any
+// order gives the same bits.
+template <int L0>
+__device__ __forceinline__ float tree_max_from(float v, int lane) {
+    if constexpr (L0 <= 5) {
+        v = fmaxf(v, tree_partner<L0>(v, lane));
+        return tree_max_from<L0 + 1>(v, lane);
+    } else {
+        return v;
+    }
+}
 
 // The value of lane l ^ 32 or l ^ 16 (one swap instruction, no LDS).
 __device__ __forceinline__ float xchg32(float v, int lane) { return tree_partner<0>(v, lane); }
@@ -248,10 +259,8 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int mask = 32; mask >= 1; mask >>= 1) v += __shfl_xor(v, mask);
-    return v;
-}
+// Sum over the 64 lanes (the tree of wave_total), every lane holding the same bits.
+__device__ __forceinline__ float wave_sum(float v) { return tree_sum_from<0>(v, (int)__lane_id()); }
+__device__ __forceinline__ float wave_max(float v) { return tree_max_from<0>(v, (int)__lane_id()); }
 
 }  // namespace kr

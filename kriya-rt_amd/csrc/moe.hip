@@ -50,8 +50,7 @@ __device__ void route_token_wave(const float (&lv)[kRoutePer], uint32_t E, uint3
     float mx = -INFINITY;  // the maximum does not depend on the order
 #pragma unroll
     for (int i = 0; i < kPer; ++i) mx = fmaxf(mx, lv[i]);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+    mx = wave_max(mx);
     float ex[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) ex[i] = (lane + 64u * i) < E ? expf(lv[i] - mx) : 0.0f;
