@@ -169,3 +169,21 @@ def test_moe_block_argument_checks(kq):
     assert need >= L.kr_q4_moe_workspace_bytes(4, 2, H, I)
     assert L.kr_q4_moe_block(ctypes.byref(router), ctypes.byref(g), ctypes.byref(u), ctypes.byref(d), E, x, 4, 2, 1,
                              0, y, kq.DTYPE_F32, 0, ws, need - 1, None) == kq.KR_E_WORKSPACE
+
+
+def test_every_option_round_trips(kq):
+    """Each KR_OPT_* the header declares is known to kr_get_option, and setting its current value back
+    succeeds; the few-token and prefill switches reject values outside their ranges."""
+    L = kq.lib()
+    hdr = open(os.path.join(ROOT, "include", "kriya_q4.h")).read()
+    opts = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define (KR_OPT_\w+) (\d+)", hdr)}
+    assert len(opts) >= 16
+    for name, code in opts.items():
+        cur = L.kr_get_option(code)
+        assert cur >= 0, name
+        assert L.kr_set_option(code, cur) == 0, (name, L.kr_last_error())
+    for name, bad in (("KR_OPT_SKINNY_GROUPS", 3), ("KR_OPT_SKINNY_DEPTH", 4), ("KR_OPT_SKINNY_DEPTH", 1),
+                      ("KR_OPT_PREFILL_OPERANDS", 2), ("KR_OPT_SPLITK_TICKETS", 2)):
+        assert L.kr_set_option(opts[name], bad) == kq.KR_E_INVALID, name
+    assert L.kr_get_option(opts["KR_OPT_SKINNY_GROUPS"]) == 2
+    assert L.kr_get_option(opts["KR_OPT_SKINNY_DEPTH"]) == 0
