@@ -76,8 +76,13 @@ __device__ __forceinline__ T ld_stream(const T *p) {
 }
 
 // ---- gated activations (q4_gemm_and_moe.metal:2064-2071)
+// SiLU g / (1 + e^-g) on the transcendental units: e^-g = 2^(-g log2 e) by v_exp_f32 and the
+// quotient as g times v_rcp_f32 (each about 1 ulp of f32, far below the bf16 rounding of the
+// outputs), instead of libm's expf and an IEEE division (about 25 instructions per value; the
+// prefill gate/up epilogue computes 32 per lane).  Large positive g gives g * rcp(1) = g, large
+// negative g gives g * rcp(inf) = -0, as the division does.
 __device__ __forceinline__ float activation(float g, int variant) {
-    if (variant == 0) return g / (1.0f + expf(-g));
+    if (variant == 0) return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-1.44269504f * g));
     if (variant == 1) {
         const float kSqrt2OverPi = 0.7978845608f;
         float cubic = fmaf(0.044715f * g, g * g, g);
