@@ -327,8 +327,92 @@ __global__ __launch_bounds__(256) void q4_mfma_splitk_reduce_kernel(MfmaArgs arg
     }
 }
 
+// The same sums and epilogue for eight consecutive outputs of a row per thread (N % 8 == 0,
+// 16-byte aligned rows, partials, outputs and bias): each split's partials are two 16-byte loads,
+// and up to kReduceBatch splits are requested before any of them is added (repeats of the last
+// split past ksplit are loaded and ignored), so that a thread waits once per batch instead of
+// once per load.  The adds run in split order from 0, as above: the bits are the same.
+constexpr uint32_t kReduceBatch = 8;
+template <int NW>
+__global__ __launch_bounds__(256) void q4_mfma_splitk_reduce8_kernel(MfmaArgs args) {
+    const MfmaProblem &P = args.p[0];
+    const uint32_t N = P.w.n, units = N >> 3;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)args.m * units) return;
+    const uint32_t m = (uint32_t)(i / units), n = (uint32_t)(i % units) * 8;
+    const size_t stride = (size_t)args.m * NW * N;
+    const float *p0 = args.partial + (size_t)m * NW * N + n;
+    float g[8] = {}, u[8] = {};
+    for (uint32_t s0 = 0; s0 < args.ksplit; s0 += kReduceBatch) {
+        f32x4 pg[kReduceBatch][2], pu[kReduceBatch][2];
+#pragma unroll
+        for (uint32_t j = 0; j < kReduceBatch; ++j) {
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(p0 + (size_t)min(s0 + j, args.ksplit - 1) * stride);
+            pg[j][0] = src[0];
+            pg[j][1] = src[1];
+            if constexpr (NW == 2) {
+                pu[j][0] = src[N / 4];
+                pu[j][1] = src[N / 4 + 1];
+            }
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kReduceBatch; ++j) {
+            if (s0 + j >= args.ksplit) break;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                g[e] += pg[j][e >> 2][e & 3];
+                if constexpr (NW == 2) u[e] += pu[j][e >> 2][e & 3];
+            }
+        }
+    }
+    float val[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) val[e] = NW == 2 ? activation(g[e], args.act) * u[e] : g[e];
+    if (P.bias) {
+        const u32x4 bw = *reinterpret_cast<const u32x4 *>(P.bias + n);
+        const uint32_t bb[4] = {bw.x, bw.y, bw.z, bw.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) val[e] += bf16_to_f32((bb[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+    }
+    const size_t o = (size_t)m * P.ldo + n;
+    if (args.out_f32) {
+        f32x4 *out = reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(P.out) + o);
+        f32x4 lo = {val[0], val[1], val[2], val[3]}, hi = {val[4], val[5], val[6], val[7]};
+        if (args.accumulate) {
+            const f32x4 o0 = out[0], o1 = out[1];
+            lo = f32x4{o0[0] + lo[0], o0[1] + lo[1], o0[2] + lo[2], o0[3] + lo[3]};
+            hi = f32x4{o1[0] + hi[0], o1[1] + hi[1], o1[2] + hi[2], o1[3] + hi[3]};
+        }
+        out[0] = lo;
+        out[1] = hi;
+    } else {
+        u32x4 *out = reinterpret_cast<u32x4 *>(reinterpret_cast<uint16_t *>(P.out) + o);
+        if (args.accumulate) {
+            const u32x4 ow = out[0];
+            const uint32_t oo[4] = {ow.x, ow.y, ow.z, ow.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) val[e] += bf16_to_f32((oo[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+        }
+        uint32_t pk[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pk[e] = f32_to_bf16(val[2 * e]) | (f32_to_bf16(val[2 * e + 1]) << 16);
+        out[0] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+    }
+}
+
 hipError_t launch_splitk_reduce(const MfmaArgs &a, int nw, hipStream_t s) {
-    const size_t total = (size_t)a.m * a.p[0].w.n;
+    const MfmaProblem &P = a.p[0];
+    const size_t total = (size_t)a.m * P.w.n;
+    const bool vec = P.w.n % 8 == 0 && P.ldo % 8 == 0 && (uintptr_t)P.out % 16 == 0 &&
+                     (uintptr_t)a.partial % 16 == 0 && (uintptr_t)P.bias % 16 == 0;
+    if (vec) {
+        const dim3 grid((unsigned)((total / 8 + 255) / 256));
+        if (nw == 2)
+            hipLaunchKernelGGL(q4_mfma_splitk_reduce8_kernel<2>, grid, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(q4_mfma_splitk_reduce8_kernel<1>, grid, dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(q4_mfma_splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a, nw);
     return hipGetLastError();
 }
@@ -347,10 +431,7 @@ static hipError_t launch_shape(MfmaArgs &a, hipStream_t s) {
         hipLaunchKernelGGL((q4_mfma_gemm_kernel<BM, BN, NW, kMfmaPartial>), grid, dim3(256), T::kLdsBytes, s, a);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        const size_t total = (size_t)a.m * a.p[0].w.n;
-        hipLaunchKernelGGL(q4_mfma_splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a,
-                           NW);
-        return hipGetLastError();
+        return launch_splitk_reduce(a, NW, s);
     }
     hipLaunchKernelGGL((q4_mfma_gemm_kernel<BM, BN, NW, kMfmaDirect>), grid, dim3(256), T::kLdsBytes, s, a);
     return hipGetLastError();
