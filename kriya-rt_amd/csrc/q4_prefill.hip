@@ -26,9 +26,13 @@
 //     fragments (no LDS round trip for W, no barrier between dequant and use);
 //     one dequantised word feeds MF matrix instructions;
 //   * X is staged in LDS by direct-to-LDS buffer loads (no VGPRs held across
-//     the step), converted to fp16 in place once per block (double buffered,
-//     one 64-column quantisation group per step, one barrier per step) and
-//     shared by the WAVES waves of the block, which split the weight rows;
+//     the step), converted to fp16 in place once per block unless the caller
+//     converted it beforehand (double buffered, two 64-column quantisation
+//     groups per step, one barrier per step) and shared by the WAVES waves of
+//     the block, which split the weight rows;
+//   * scales and biases arrive in 16-byte blocks that cover four steps of a
+//     row: the kernel is paced by memory requests more than by bytes, and a
+//     4-byte load per row and step was one request for 4 bytes;
 //   * the k order inside each 8-column unit is the nibble-pair order of the
 //     dequantiser, (e0 e4 e1 e5 e2 e6 e3 e7), applied to X when it is staged,
 //     so neither side permutes in the inner loop (a dot product does not depend
@@ -59,6 +63,15 @@ namespace kr {
 namespace {
 
 using rsrc_t = __amdgpu_buffer_rsrc_t;
+
+template <class F, int... J>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, J...>) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
@@ -131,11 +144,13 @@ struct PrefillTile {
 // weights requested together D steps ahead, both get D steps of latency.
 // SW: quantisation groups (64 columns) per step.  With SW = 2 a lane's
 // weights of a step are one 16-byte load (32 nibbles: four MFMA slices) and
-// its scales and biases one 4-byte pair each: half the load instructions of
-// SW = 1, whose lanes load 8 bytes and two 2-byte values per 64 columns.
-// KW: groups of WAVES waves that split the block's steps (group k takes steps
-// k, k + KW, ...; each group has its own X ring) and add their accumulators
-// through LDS in group order at the end.  Shapes with few tiles (N = 2048)
+// its scales and biases come in 16-byte blocks of four steps (below): far
+// fewer load instructions and memory requests than SW = 1, whose lanes load
+// 8 bytes and two 2-byte values per 64 columns.
+// KW: groups of WAVES waves that split the block's steps (each group has its
+// own X ring) and add their accumulators through LDS in group order at the
+// end.  With SW = 2 and D = 1 group k takes the k-th contiguous part of the
+// steps; otherwise steps k, k + KW, ....  Shapes with few tiles (N = 2048)
 // get KW waves per tile instead of one: more waves per SIMD to overlap the
 // latencies of each wave's step, with no workspace.
 template <int MF, int NF, int WAVES, int NW, int OCC, int EPI, int D, int SW, int KW>
@@ -347,7 +362,76 @@ __global__ __launch_bounds__(64 * WAVES * KW, OCC) void q4_prefill_kernel(MfmaAr
         }
     };
 
-    if (g_begin < g_end) {
+    if constexpr (SW == 2 && D == 1) {
+      if (g_begin < g_end) {
+        // 128-column steps, one step of look-ahead, scales and biases in blocks of four steps: a
+        // lane's 16-byte load holds the scale (or bias) words of four consecutive steps of its row
+        // (groups 2 g .. 2 g + 7), the same 16 bytes for the row's four lanes, so a row costs one
+        // memory request per four steps instead of one per step (per-step 4-byte loads were 12 %
+        // of the gate/up time: the kernel is paced by requests, not bytes).  The block of steps
+        // i + 1 .. i + 4 is requested at step i = 3 mod 4 (one step ahead, as the words), after
+        // that step's words were taken from the previous block; reads past the end of the scale
+        // arrays return zeros (buffer range check) and are never used.  A group's steps are
+        // contiguous (group k takes the k-th part of the range), and the loop runs whole blocks
+        // of four: steps past the group's part load (clamped) and wait but do not compute.
+        constexpr int NB = 2;
+        constexpr int kQLoads = NF, kSBLoads = 2 * NF;
+        WRegs w[NB];
+        u32x4 sblk[NF], bblk[NF];
+        const uint32_t nsteps = (g_end - g_begin + KW - 1) / KW;
+        const uint32_t gfirst = g_begin + kg * nsteps;
+        auto gstep = [&](uint32_t i) { return gfirst + i; };
+        auto gc = [&](uint32_t g) { return min(g, GS - 1); };
+        auto load_q = [&](uint32_t g, WRegs &r) {
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const int mi = f / FPM, fi = f % FPM;
+                const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq[mi], oq[fi], g * 64, 0));
+                r.q[f][0] = v.x;
+                r.q[f][1] = v.y;
+                r.q[f][2] = v.z;
+                r.q[f][3] = v.w;
+            }
+        };
+        auto load_sb = [&](uint32_t g) {
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const int mi = f / FPM, fi = f % FPM;
+                sblk[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs[mi], os[fi], g * 4, 0));
+                bblk[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb[mi], os[fi], g * 4, 0));
+            }
+        };
+        dma_x(gc(gstep(0)), 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_q(gc(gstep(0)), w[0]);
+        load_sb(gc(gstep(0)));
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kQLoads + kSBLoads) : "memory");
+        convert_x(0);
+        __syncthreads();
+        for (uint32_t i0 = 0; i0 < nsteps; i0 += 4) {
+            static_for<4>([&](auto U) {
+                constexpr int u = U;
+                constexpr int b = u & 1;
+                const uint32_t i = i0 + (uint32_t)u;
+                dma_x(gc(gstep(i + 1)), b ^ 1);
+                __builtin_amdgcn_sched_barrier(0);
+                load_q(gc(gstep(i + 1)), w[b ^ 1]);
+#pragma unroll
+                for (int f = 0; f < NF; ++f) {
+                    w[b].s[f] = sblk[f][u];
+                    w[b].b[f] = bblk[f][u];
+                }
+                if constexpr (u == 3) load_sb(gc(gstep(i + 1)));
+                __builtin_amdgcn_sched_barrier(0);  // keep the loads at the top of the step
+                if (i < nsteps && gstep(i) < g_end) compute(b, w[b]);
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kQLoads + (u == 3 ? kSBLoads : 0)) : "memory");
+                convert_x(b ^ 1);
+                __syncthreads();
+            });
+        }
+      }
+    } else if (g_begin < g_end) {
         constexpr int NB = D + 1;
         constexpr int kWLoads = 3 * NF;
         // loads issued after the X slice of a step: its weights and the later D - 1 (X, weights) pairs
