@@ -213,7 +213,9 @@ void choose_split_k(MfmaArgs &a, int bm, float *partial) {
     const uint32_t rows = prefill ? prefill_block_m(a.p[0].w2.qw != nullptr) : (uint32_t)bm_rows(bm);
     const uint32_t cols = prefill ? prefill_block_rows(a.p[0].w2.qw != nullptr) : (uint32_t)bn_of(bm, false);
     const uint32_t tiles = ((a.m + rows - 1) / rows) * ((a.p[0].w.n + cols - 1) / cols);
-    const uint32_t target = 2u * (uint32_t)device_cus();
+    // the prefill kernel's split tiles: about one block per CU (fewer partials to reduce); the
+    // tiled kernel: two
+    const uint32_t target = (prefill ? 1u : 2u) * (uint32_t)device_cus();
     uint32_t split = 1;
     while (split < kMaxSplitK && tiles * split < target && groups / (split * 2) >= 8) split *= 2;
     if (split > 1) {

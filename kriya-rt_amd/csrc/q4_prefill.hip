@@ -731,11 +731,13 @@ static hipError_t launch_prefill_shape(MfmaArgs &a, hipStream_t s) {
 //   plain:    64 token rows x (4 waves x 16 rows), one step of look-ahead, 4
 //             waves per SIMD: the N = 2048 projections are short of blocks with
 //             larger tiles (96 x 128: down 145 us, o 33 us; 64 x 64: 72 / 17.6 us);
-//   split K:  96 token rows x (4 waves x 32 rows), one step of look-ahead, when
-//             the MLP's workspace lets the down projection split K over blocks.
+//   split K: 128 token rows x (4 waves x 32 rows), one step of look-ahead, when
+//             the MLP's workspace lets the down projection split K over blocks
+//             (K split to about one block per CU: cfg2 down 4 ways, 37.0 us + 5.3 us
+//             of reduction, against 96-row tiles split 8 ways, 38.9 + 7.2 us).
 using GateUpShape = PrefillTile<8, 2, 4, 2>;
 using PlainShape = PrefillTile<4, 1, 4, 1>;
-using SplitShape = PrefillTile<6, 2, 4, 1>;  // plain projections whose K is split over blocks
+using SplitShape = PrefillTile<8, 2, 4, 1>;  // plain projections whose K is split over blocks
 
 uint32_t prefill_block_m(bool gate_up) { return gate_up ? GateUpShape::kBM : SplitShape::kBM; }
 uint32_t prefill_block_rows(bool gate_up) { return gate_up ? GateUpShape::kBN : SplitShape::kBN; }
@@ -756,11 +758,11 @@ hipError_t launch_prefill(MfmaArgs &a, hipStream_t s) {
     const uint32_t gps = a.ksplit > 1 ? a.groups_per_split : a.k / 64;
     if (tuning().prefill_kernel == 2 || a.k % 128 != 0 || gps % 2 != 0) {  // 64 columns per step
         if (gate_up) return launch_prefill_shape<8, 2, 4, 2, 3, 2, 1>(a, s);
-        if (a.ksplit > 1) return launch_prefill_shape<6, 2, 4, 1, 4, 2, 1>(a, s);
+        if (a.ksplit > 1) return launch_prefill_shape<8, 2, 4, 1, 3, 2, 1>(a, s);
         return launch_prefill_shape<4, 1, 4, 1, 4, 2, 1>(a, s);
     }
     if (gate_up) return launch_prefill_shape<8, 2, 4, 2, 2, 1, 2>(a, s);
-    if (a.ksplit > 1) return launch_prefill_shape<6, 2, 4, 1, 2, 1, 2>(a, s);
+    if (a.ksplit > 1) return launch_prefill_shape<8, 2, 4, 1, 2, 1, 2>(a, s);
     // Fewer tiles than two per compute unit (the N = 2048 .. 2560 projections at M = 512): two
     // groups of waves per tile split its steps (qkv 20.2 -> 19.0 us; four groups: 21.8 us).
     uint32_t tiles = 0;
