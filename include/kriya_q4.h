@@ -63,7 +63,8 @@ extern "C" {
 #define KR_DTYPE_F32 1
 
 /* ---- gated activations (descriptor.rs ActivationVariant; encoder.rs:2718-2722) ---- */
-#define KR_ACT_SWIGLU 0 /* silu(g) * u                      */
+#define KR_ACT_SWIGLU 0 /* silu(g) * u; silu(g) = g / (1 + e^-g) computed as g * rcp(1 + exp2(-g log2 e))
+                         * on the hardware exp2 and reciprocal (about 1 ulp of f32 each)               */
 #define KR_ACT_GEGLU 1  /* gelu_tanh(g) * u                 */
 #define KR_ACT_RELU 2   /* max(g, 0) * u                    */
 
