@@ -51,8 +51,8 @@
 // Gate/up: a wave's fragments are FPM gate fragments followed by FPM up
 // fragments of the same rows, so act(g) * u is formed lane-locally.
 // Block ids are remapped so that the M tiles of one N tile run on one XCD and
-// share its L2; split-K (grid.y) writes f32 partials that
-// q4_mfma_splitk_reduce_kernel sums in split order.
+// share its L2; split-K (grid.y) writes f32 partials that the reduction
+// launch (launch_splitk_reduce) sums in split order.
 #include <type_traits>
 
 #include "kr_internal.hpp"

@@ -41,7 +41,8 @@
 // Gate/up: a tile holds 8 gate rows (lanes 0-7) and the same 8 up rows (lanes
 // 8-15); the epilogue pairs column c with column c + 8.
 // K longer than one slab is split over blocks (one slab each) and the f32
-// partials are reduced in slab order by q4_mfma_splitk_reduce_kernel.
+// partials are reduced in slab order, by the last block of each run (tickets)
+// or by a second launch (launch_splitk_reduce).
 // Grouped mode (MoE): the weight matrix stacks E experts of expert_rows rows;
 // offsets[E+1] and the expert-sorted assignment list select, per expert, the
 // token rows to gather (X row = sorted[p] / x_div, or p) and where each result
