@@ -168,6 +168,27 @@ def test_mlp_prefill_split_k(kq):
     assert_rms_close(runs[0] - O.bf16_to_f32(h0), delta, what="mlp m=96")
 
 
+def test_splitk_reduction_paths_bitwise(kq):
+    """The split-K reduction has a vector form (eight outputs per thread, 16-byte aligned rows) and a
+    scalar form (an output that is not 16-byte aligned); both add the partials in split order from 0,
+    so an h offset by one f32 element gives the same bits as an aligned one."""
+    s = synth()
+    case("mlp m=96 split-K down: h 16-byte aligned vs offset by one element, bitwise")
+    g, u = s.q4_weight(1408, 512, 2611), s.q4_weight(1408, 512, 2612)
+    d = s.q4_weight(512, 1408, 2613)
+    h0 = s.bf16_normal((96, 512), 2614)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    outs = []
+    for off in (0, 1):
+        buf = torch.zeros(96 * 512 + 4, dtype=torch.float32, device="cuda")
+        h = buf[off:off + 96 * 512].view(96, 512)
+        h.copy_(torch.from_numpy(O.bf16_to_f32(h0)).cuda())
+        assert (h.data_ptr() % 16 == 0) == (off == 0)
+        kq.mlp(G, U, D, h, x=dev_bf16(h0))
+        outs.append(h.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("m", [64, 512])
 def test_prefill_kernels_agree(kq, m):
     """The register-dequant prefill kernel and the LDS-dequant tiled kernel give the same sums
