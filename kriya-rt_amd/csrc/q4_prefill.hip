@@ -64,15 +64,6 @@ namespace {
 
 using rsrc_t = __amdgpu_buffer_rsrc_t;
 
-template <class F, int... J>
-__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, J...>) {
-    (f(std::integral_constant<int, J>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 __device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes, 0x00020000);
 }

@@ -63,16 +63,6 @@ constexpr int kSkinnyWaves = 8;
 constexpr int kSkinnyPieces = 2;                                // 128-column pieces per wave
 constexpr int kSlabCols = kSkinnyWaves * kSkinnyPieces * 128;  // K columns per block
 
-// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
-template <class F, int... J>
-__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, J...>) {
-    (f(std::integral_constant<int, J>{}), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 __device__ __forceinline__ uint32_t opq_s(uint32_t v) {
     uint32_t r;
     asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
