@@ -83,6 +83,36 @@ def graph_time_per_step(torch, fn, nsteps, replays, warmup_replays=2):
     return start.elapsed_time(end) * 1e-3 / (replays * nsteps)
 
 
+# A bounded spin kernel (torch.cuda._sleep) holds the stream while the host enqueues a chain of launches, so the
+# GPU then runs them back to back with no host gaps.  ~50 M shader cycles is ~20 ms at MI355X clocks, far more than
+# the host needs to enqueue CHAIN_LAUNCHES launches (longer chains hold proportionally longer).
+HOLD_CYCLES = 50_000_000
+CHAIN_LAUNCHES = 640  # launches per timed chain (the host queues them in a few ms)
+
+
+def chain_time_per_launch(torch, fn, n, reps=3):
+    """Average duration of one launch of fn(i): n eager launches fn(0) .. fn(n - 1) are queued behind a bounded spin
+    kernel and bracketed by two HIP events on the launch stream; the median over `reps` chains of elapsed / n.
+    rocprofv3 --kernel-trace reports the same average duration for the kernel (within ~1 %), whereas replays of a
+    HIP graph of the chain run a few per cent apart from it.  Returns (seconds per launch, starved) where starved is
+    True if a chain's hold ended before the host had queued the whole chain (then host gaps may be included)."""
+    for i in range(min(n, 3)):
+        fn(i)
+    torch.cuda.synchronize()
+    times, starved = [], False
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(HOLD_CYCLES * max(1, -(-n // CHAIN_LAUNCHES)))
+        a.record()
+        for i in range(n):
+            fn(i)
+        b.record()
+        starved |= a.query()  # the hold already ended: the GPU may have waited for the host
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) * 1e-3 / n)
+    return float(np.median(times)), starved
+
+
 def graph_time_exact(torch, fn, steps, warmup):
     """The contract's timed region: `warmup` untimed steps, then EXACTLY `steps` steps fn(0) .. fn(steps - 1)
     captured in one HIP graph and replayed once, bracketed by device synchronisations.  Returns seconds per
@@ -130,7 +160,7 @@ def bench_mlp(kq, torch, synth, B, copies, steps, warmup):
     alg_bytes = weight_bytes + 2 * 2 * B * H  # weights + h read + h write
     out = {"B": B, "s_per_step": t_step, "alg_bytes": alg_bytes, "gbs": alg_bytes / t_step / 1e9, "steps": steps}
 
-    # per-kernel average durations (each kernel alone over the rotating copies)
+    # per-kernel average durations (each kernel alone over the rotating copies, as an eager chain behind a hold)
     act = torch.empty((B, I), dtype=torch.bfloat16, device="cuda")
 
     def gate_up(i):
@@ -141,11 +171,16 @@ def bench_mlp(kq, torch, synth, B, copies, steps, warmup):
         _, _, d = rot.sets[i % len(rot)]
         kq.q4_linear(d, act, y=h, accumulate=True)
 
-    t_gu = graph_time_per_step(torch, gate_up, nsteps, replays, warm)
-    out["kernels"] = {"gate_up_act": {"s": t_gu, "alg_bytes": 2 * Q4_BYTES(I, H) + 2 * B * H + 2 * B * I}}
+    chain = max(steps, CHAIN_LAUNCHES)
+    t_gu, st_gu = chain_time_per_launch(torch, gate_up, chain)
+    out["kernels"] = {"gate_up_act": {"s": t_gu, "alg_bytes": 2 * Q4_BYTES(I, H) + 2 * B * H + 2 * B * I,
+                                      "graph_s": graph_time_per_step(torch, gate_up, nsteps, replays, warm),
+                                      "starved": st_gu}}
     if B == 1:  # m = 1: the down projection is one launch of its own (the GEMV with accumulate)
-        t_dn = graph_time_per_step(torch, down, nsteps, replays, warm)
-        out["kernels"]["down_acc"] = {"s": t_dn, "alg_bytes": Q4_BYTES(H, I) + 2 * B * I + 4 * B * H}
+        t_dn, st_dn = chain_time_per_launch(torch, down, chain)
+        out["kernels"]["down_acc"] = {"s": t_dn, "alg_bytes": Q4_BYTES(H, I) + 2 * B * I + 4 * B * H,
+                                      "graph_s": graph_time_per_step(torch, down, nsteps, replays, warm),
+                                      "starved": st_dn}
     for k in out["kernels"].values():
         k["gbs"] = k["alg_bytes"] / k["s"] / 1e9
     return out
@@ -164,7 +199,7 @@ def stream_floor(kq, torch, nbytes, copies, steps, warmup):
     def rd(i):
         kq.stream_read(bufs[i % copies], hits=hits)
 
-    t = graph_time_per_step(torch, rd, copies, max(1, steps // copies), max(1, warmup // copies))
+    t, _ = chain_time_per_launch(torch, rd, max(steps, CHAIN_LAUNCHES))
     del bufs
     return t
 
@@ -357,7 +392,7 @@ def profile_run(kq, torch, synth, what, reps=8):
       prefill: cfg2's layer at M = 512 (q/k/v in one launch, o accumulated, gate/up + SwiGLU, split-K down);
       few:     cfg1's MLP at B = 16 (few-token gate/up, down with the in-launch split-K reduction) and cfg4's
                grouped experts at T = 64;
-      gemv:    cfg1's MLP at B = 1 (the headline kernels)."""
+      gemv:    cfg1's MLP at B = 1 (the headline kernels) and cfg0's GEMV."""
     H, I, KV = synth.HIDDEN, synth.INTER, 256
     if what == "prefill":
         M = 512
@@ -384,6 +419,12 @@ def profile_run(kq, torch, synth, what, reps=8):
         for i in range(reps):
             g, u, d = rot.sets[i % 2]
             kq.mlp(g, u, d, h, x=xs, workspace=ws)
+        if what == "gemv":  # config 0: one GEMV 11008 x 2048 into bf16
+            rot0 = Rotation(kq, torch, [synth.q4_weight(11008, 2048, 0)], 2)
+            x0 = torch.from_numpy(synth.bf16_normal((1, 2048), 1).view(np.int16)).cuda().view(torch.bfloat16)
+            y0 = torch.empty((1, 11008), dtype=torch.bfloat16, device="cuda")
+            for i in range(reps):
+                kq.q4_linear(rot0.sets[i % 2][0], x0, y=y0)
         if what == "few":
             E, K, T, Im = 60, 4, 64, 1408
             mrot = Rotation(kq, torch, [synth.q4_weight(E * Im, H, 4001), synth.q4_weight(E * Im, H, 4002),
@@ -455,12 +496,17 @@ def main():
         "config": {"workload": "cfg1_fused_mlp_decode_B1", "hidden": 2048, "intermediate": 11008, "batch": 1,
                    "weights": "Q4_G64 gate/up [11008,2048], down [2048,11008]",
                    "launches_per_step": 2, "graph": "HIP graph replay"},
-        "roofline": {"bound": "hbm", "kernel": "q4_gemv_wave_kernel<R,1,kGateUpBF16> (gate+up+silu fused, m=1)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "kr::q4_gemv_wave_kernel<2, 1, 5, false, false> (gate+up+SiLU fused, m=1)",
                      "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "traffic_source": "profiles/pmc_traffic_q4_gemv_cfg1_B1.md (rocprofv3 FETCH_SIZE/WRITE_SIZE, "
                                        "copy-calibrated)",
-                     "alg_bytes_per_launch": dom["alg_bytes"], "avg_launch_us": round(dom["s"] * 1e6, 3)},
+                     "alg_bytes_per_launch": dom["alg_bytes"], "avg_launch_us": round(dom["s"] * 1e6, 3),
+                     "timing": "HIP events around an eager chain of launches over the rotating copies, queued "
+                               "behind a bounded spin kernel (the duration rocprofv3 --kernel-trace reports)",
+                     "chain_starved": dom["starved"],
+                     "graph_interval_us": round(dom["graph_s"] * 1e6, 3)},
         "cpu_baseline": None,
     }
     log("streaming floor (plain reads of the same byte counts)")
@@ -471,6 +517,8 @@ def main():
     extra = {"cfg1_B1": {"step_us": round(head["s_per_step"] * 1e6, 3), "gbs": round(head["gbs"], 1),
                          "frac_hbm": round(head["gbs"] / HBM_PEAK_GBS, 4),
                          "kernels_us": {k: round(v["s"] * 1e6, 3) for k, v in head["kernels"].items()},
+                         "kernels_graph_interval_us": {k: round(v["graph_s"] * 1e6, 3)
+                                                       for k, v in head["kernels"].items()},
                          "kernels_gbs": {k: round(v["gbs"], 1) for k, v in head["kernels"].items()},
                          "stream_floor_us": {k: round(v * 1e6, 3) for k, v in floors.items()}}}
     if not args.quick:

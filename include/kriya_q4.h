@@ -212,8 +212,7 @@ int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matr
               const uint16_t *x, void *h, int h_dtype, uint32_t m, int activation,
               void *workspace, size_t workspace_bytes, void *stream);
 
-/* ---- dense MLP without a workspace (no counterpart in the reference, whose
- *      executor pre-allocates its scratch buffers, encoder.rs:1957-2035) ----
+/* ---- dense MLP without a workspace (no counterpart in the reference) ----
  * For callers that cannot allocate device memory: code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc.  Same arguments, results
  * and kernels as kr_q4_mlp, but the workspace is a device array inside the

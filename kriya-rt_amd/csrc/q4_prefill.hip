@@ -234,11 +234,16 @@ __global__ __launch_bounds__(64 * WAVES * KW, OCC) void q4_prefill_kernel(MfmaAr
         }
     };
     // Block-wide OR without LDS of its own (a static LDS array would cost the 64-row shape one of
-    // its five blocks per CU): each wave's ballot goes to a flag byte in X buffer 0, a barrier, then
-    // every lane reads the WAVES flags.  Only after the last step, when no load writes the buffers.
+    // its five blocks per CU): each wave's ballot goes to a flag byte in X buffer 0 (inside wave 0's
+    // slice of it), a barrier, then every lane reads the WAVES flags.  Only after the last step.  The
+    // 64-column path's last step requests a clamped look-ahead slice that nothing waits for, and it
+    // may land in buffer 0: every wave waits for its direct-to-LDS loads, and a barrier makes sure all
+    // have landed, before any flag byte is written.
     auto block_any = [&](bool pred) -> bool {
         int8_t *flags = reinterpret_cast<int8_t *>(lds);
         const bool wave_any = __ballot(pred) != 0ull;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
         if (lane == 0) flags[wid] = wave_any ? 1 : 0;
         __syncthreads();
         bool any = false;

@@ -27,6 +27,7 @@
 #include <map>
 #include <memory>
 #include <string>
+#include <unordered_set>
 #include <utility>
 #include <vector>
 
@@ -219,6 +220,9 @@ class JParser {
                     ++p_;
                     break;
                 }
+                // Duplicate keys are rejected through a hash set of the object's keys: linear in the key count
+                // (a header or weight map names up to ~10^5 tensors).
+                std::unordered_set<std::string> seen;
                 for (;;) {
                     ws();
                     std::string key;
@@ -228,8 +232,7 @@ class JParser {
                     ++p_;
                     JVal child;
                     if (!value(child)) return false;
-                    for (const auto &kv : v.obj)
-                        if (kv.first == key) return fail("duplicate key in an object");
+                    if (!seen.insert(key).second) return fail("duplicate key in an object");
                     v.obj.emplace_back(std::move(key), std::move(child));
                     ws();
                     if (p_ < e_ && *p_ == ',') {

@@ -334,3 +334,123 @@ def test_skinny_depth_bitwise(kq, m):
         assert_rms_close(res[0][3 * i], O.q4_gate_up_act(O.Q4Planar(*g), O.Q4Planar(*u), x), what=f"gate/up {shapes[i]}")
         assert_rms_close(res[0][3 * i + 2], O.q4_matmul(O.Q4Planar(*g), x), what=f"linear {shapes[i]}")
     assert_rms_close(res[0][-1], O.q4_mlp(O.Q4Planar(*mg), O.Q4Planar(*mu), O.Q4Planar(*md), xm), what="mlp")
+
+
+def test_mlp_config2_full_shape(kq):
+    """kr_q4_mlp at config 2's MLP shape (M = 512, hidden 2048, inter 11008; encoder.rs:2851-2906), the call
+    bench.py times: the fused gate/up SwiGLU prefill epilogue, then the down projection split over K = 11008
+    into f32 partials summed in split order.  Into an f32 residual, each row within 1e-2 of its own RMS against
+    the oracle, and bit-identical with the fp16 operands converted once per call (option 1, the default) or
+    per block (option 0)."""
+    s = synth()
+    M, H, I = 512, 2048, 11008
+    case(f"mlp cfg2 full shape M={M} hidden {H} inter {I}, split-K down, both operand options")
+    g, u, d = s.q4_weight(I, H, 2005), s.q4_weight(I, H, 2006), s.q4_weight(H, I, 2007)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    x = s.bf16_normal((M, H), 2105)
+    h0 = O.bf16_to_f32(s.bf16_normal((M, H), 2106))
+    ws = kq.mlp_workspace(M, H, I)
+    lib = kq.lib()
+    res = {}
+    try:
+        for opt in (0, 1):
+            assert lib.kr_set_option(kq.OPT_PREFILL_OPERANDS, opt) == 0
+            h = torch.from_numpy(h0).cuda()
+            kq.mlp(G, U, D, h, x=dev_bf16(x), workspace=ws)
+            res[opt] = h.cpu().numpy()
+    finally:
+        lib.kr_set_option(kq.OPT_PREFILL_OPERANDS, 1)
+    assert np.array_equal(res[0].view(np.uint32), res[1].view(np.uint32))
+    delta = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), x)
+    got = res[1].astype(np.float64) - h0
+    worst = 0.0
+    for i in range(M):
+        worst = max(worst, assert_rms_close(got[i], delta[i], what=f"mlp cfg2 row {i}") / rms(delta[i]))
+    print(f"mlp cfg2: worst row max err {worst:.2e} of the row's rms", flush=True)
+
+
+def test_consolidated_qkv_matches_separate_projections(kq):
+    """Restates test_shader_compile.rs:3185-3286: the q, k and v rows of one layer live in ONE Q4_G64 buffer
+    (192 x 64, weights ((idx % 31) - 15) * 0.02 quantised by quantize_f32_to_q4_group64), bound to the device
+    from its split planes with the nibble plane used in place; the fused QKV call over its three row ranges
+    passes the reference's own check (|f32 dot of the dequantised q rows with the f32 input - the bf16
+    output| < 0.05) and gives the bits of the three separate projections."""
+    k, q_dim, kv_dim = 64, 64, 64
+    total = q_dim + 2 * kv_dim
+    case("consolidated qkv 192 x 64 from split planes in place vs separate projections")
+    wflat = ((np.arange(total * k) % 31).astype(np.float32) - np.float32(15.0)) * np.float32(0.02)
+    blocks = O.quantize_q4_g64(wflat)
+    qs, sb = O.split_blocks36(blocks)
+    qs_dev = torch.from_numpy(qs.ravel().copy()).cuda()
+    sb_dev = torch.from_numpy(sb.view(np.uint8).ravel().copy()).cuda()
+    W = kq.Q4Matrix.from_split(qs_dev, sb_dev, total, k, in_place=True)
+    assert W.qw.data_ptr() == qs_dev.data_ptr()
+    inp = np.sin(np.arange(k, dtype=np.float32) * np.float32(0.05)).astype(np.float32)
+    x = O.f32_to_bf16(inp)[None, :]
+    ranges = ((0, q_dim), (q_dim, q_dim + kv_dim), (q_dim + kv_dim, total))
+    outs = kq.qkv(*(W.rows(lo, hi) for lo, hi in ranges), dev_bf16(x), out_dtype=kq.DTYPE_BF16)
+    deq = O.dequant_blocks36(blocks).reshape(total, k)
+    out_q = O.bf16_to_f32(host_bits(outs[0]).ravel())
+    for row in range(q_dim):
+        dot = np.float32(0.0)
+        for c in range(k):  # the reference's sequential f32 dot
+            dot = np.float32(dot + deq[row, c] * inp[c])
+        assert abs(float(dot) - float(out_q[row])) < 0.05, f"q row {row}: cpu {dot} gpu {out_q[row]}"
+    for i, (lo, hi) in enumerate(ranges):
+        sep = kq.q4_linear(W.rows(lo, hi), dev_bf16(x), out_dtype=kq.DTYPE_BF16)
+        assert np.array_equal(host_bits(sep), host_bits(outs[i])), f"projection {i}"
+
+
+@pytest.mark.parametrize("m", [1, 16, 512])
+def test_consolidated_qkv_config3_shape(kq, m):
+    """Config 3's attention projections (q [2048, 2048], k and v [256, 2048], with bf16 biases) concatenated in
+    one buffer that is bound from split planes in place: the row-range views give the bits of separately bound
+    matrices, and the oracle's results within the bar."""
+    s = synth()
+    case(f"consolidated qkv cfg3 shape from split planes, m={m}")
+    shapes = (2048, 256, 256)
+    parts = [s.q4_weight(n, 2048, 2440 + i) for i, n in enumerate(shapes)]
+    cat = O.Q4Planar(*(np.concatenate([p[j] for p in parts]) for j in range(3)))
+    qs, sb = O.split_blocks36(O.planar_to_blocks36(cat))
+    qs_dev = torch.from_numpy(qs.ravel().copy()).cuda()
+    sb_dev = torch.from_numpy(sb.view(np.uint8).ravel().copy()).cuda()
+    W = kq.Q4Matrix.from_split(qs_dev, sb_dev, cat.n, 2048, in_place=True)
+    bs = [s.bf16_normal((n,), 2450 + i, std=0.1) for i, n in enumerate(shapes)]
+    x = s.bf16_normal((m, 2048), 2460 + m)
+    bounds = np.cumsum((0,) + shapes)
+    views = [W.rows(int(bounds[i]), int(bounds[i + 1])) for i in range(3)]
+    got = kq.qkv(*views, dev_bf16(x), *(dev_bf16(b) for b in bs), out_dtype=kq.DTYPE_F32)
+    sep = kq.qkv(*(q4_dev(kq, p) for p in parts), dev_bf16(x), *(dev_bf16(b) for b in bs), out_dtype=kq.DTYPE_F32)
+    for i, name in enumerate("qkv"):
+        assert torch.equal(got[i].view(torch.int32), sep[i].view(torch.int32)), name
+        want = O.q4_matmul(O.Q4Planar(*parts[i]), x) + O.bf16_to_f32(bs[i])[None, :]
+        assert_rms_close(got[i].cpu().numpy(), want, what=f"{name} m={m}")
+
+
+@pytest.mark.parametrize("opt", [0, 2])
+def test_prefill_fp16_overflow_fallback_k2048(kq, opt):
+    """x beyond fp16's range (65504) sends a prefill block to its exact f32 fallback, chosen by a block-wide
+    OR whose flag bytes sit in an X buffer.  With 64-column steps (option 2) K = 2048 has 32 steps, so the
+    last step's clamped look-ahead slice goes to buffer (32 + 1) % 3 = 0, where the flags are: the
+    fallback still triggers for the overflowing rows' blocks, and no block takes it by mistake (every row
+    within the bar of the oracle, also without overflow)."""
+    s = synth()
+    m, n, k = 64, 256, 2048
+    case(f"prefill fp16-overflow fallback, option {opt}, m={m} n={n} k={k}")
+    wq = s.q4_weight(n, k, 2720)
+    x = s.bf16_normal((m, k), 2721)
+    big = O.bf16_to_f32(x).copy()
+    big[5] *= 1e5
+    xs = {"normal": x, "overflow": O.f32_to_bf16(big)}
+    w = q4_dev(kq, wq)
+    lib = kq.lib()
+    try:
+        assert lib.kr_set_option(kq.OPT_PREFILL_KERNEL, opt) == 0
+        for name, xv in xs.items():
+            want = O.q4_matmul(O.Q4Planar(*wq), xv)
+            got = kq.q4_linear(w, dev_bf16(xv), out_dtype=kq.DTYPE_F32).cpu().numpy()
+            assert np.all(np.isfinite(got)), name
+            for i in range(m):
+                assert_rms_close(got[i], want[i], what=f"{name} row {i}")
+    finally:
+        lib.kr_set_option(kq.OPT_PREFILL_KERNEL, 0)

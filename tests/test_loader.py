@@ -218,3 +218,39 @@ def test_validate_dense_checkpoint(ld, tmp_path):
     bad = ("model.layers.0.post_attention_layernorm.weight", (h // 2, 2))
     with ld.Archive(dense_checkpoint(tmp_path / "shape", CFG, reshape=bad)) as a:
         raises(ld, ld.KR_E_FORMAT, a.validate_dense, **kw, match="post_attention_layernorm")
+
+
+def test_large_headers_open_in_linear_time(ld, tmp_path):
+    """A MoE checkpoint names ~10^5 tensors: a 100k-entry header, and a sharded index of 100k entries over two
+    shards, open within a few seconds (duplicate keys are found through a hash set, not by rescanning every
+    earlier key), and a duplicate placed last in a 100k-entry header is still rejected."""
+    import time
+
+    n = 100_000
+    names = [f"model.layers.{i // 1000}.mlp.experts.{i % 1000}.w" for i in range(n)]
+    big = {nm: ("U8", (1,), bytes([i & 0xFF])) for i, nm in enumerate(names)}
+    p = tmp_path / "big.safetensors"
+    st.write(p, big)
+    t0 = time.perf_counter()
+    with ld.Archive(p) as a:
+        assert len(a.names()) == n
+        assert a.host_bytes(names[-1]).tobytes() == bytes([(n - 1) & 0xFF])
+    t_file = time.perf_counter() - t0
+    half = n // 2
+    st.write(tmp_path / "model-00001-of-00002.safetensors", {nm: big[nm] for nm in names[:half]})
+    st.write(tmp_path / "model-00002-of-00002.safetensors", {nm: big[nm] for nm in names[half:]})
+    wm = {nm: f"model-0000{1 + (i >= half)}-of-00002.safetensors" for i, nm in enumerate(names)}
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": wm}))
+    t0 = time.perf_counter()
+    with ld.Archive(tmp_path) as a:
+        assert len(a.names()) == n
+        assert a.info(names[-1])["shard"] == "model-00002-of-00002.safetensors"
+    t_index = time.perf_counter() - t0
+    print(f"100k-entry header {t_file:.2f} s, 100k-entry index over two shards {t_index:.2f} s")
+    assert t_file < 5.0 and t_index < 10.0, (t_file, t_index)
+    entries = ", ".join(f'"{nm}": {{"dtype": "U8", "shape": [1], "data_offsets": [{i}, {i + 1}]}}'
+                        for i, nm in enumerate(names))
+    dup = f'{{{entries}, "{names[0]}": {{"dtype": "U8", "shape": [1], "data_offsets": [0, 1]}}}}'
+    p2 = tmp_path / "dup.safetensors"
+    st.write(p2, {}, raw_header=dup, extra_data=bytes(n))
+    raises(ld, ld.KR_E_FORMAT, ld.Archive, p2, match="duplicate key")
