@@ -276,10 +276,9 @@ def bench_moe_cfg4(kq, torch, synth, copies, steps):
         torch.cuda.synchronize()
         active = int((r.counts > 0).sum().item())
 
-        def step(i):
+        def step(i):  # routing from the logits, then the experts (kr_q4_moe_route_experts)
             g, u, d = rot.sets[i % len(rot)]
-            kq.moe_route(logits, K, True, out=r)
-            kq.moe_experts(g, u, d, E, x, r, y=y, workspace=ws)
+            kq.moe_route_experts(g, u, d, E, x, logits, K, True, out=r, y=y, workspace=ws)
 
         def experts(i):
             g, u, d = rot.sets[i % len(rot)]

@@ -121,6 +121,12 @@ const char *kr_last_error(void);
                                          * 0 (default) three register buffers of tile words (two tiles
                                          * in flight) when a block's run holds >= 6 tiles, else two;
                                          * 2 or 3 forces that depth.  Bitwise the same results. */
+#define KR_OPT_MOE_COMBINE 17          /* kr_q4_moe_experts on the routed GEMV path (option 10) with
+                                         * topk <= 4: 1 (default) the combine is folded into the down
+                                         * projection's launch; 0 a launch of its own.  Bitwise the same. */
+#define KR_OPT_MOE_ROUTE_FUSED 18      /* kr_q4_moe_route_experts / kr_q4_moe_block with one token on the
+                                         * routed GEMV path: 1 (default) the routing runs inside the gate/up
+                                         * launch; 0 the routing kernel first.  Bitwise the same. */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 
@@ -284,11 +290,29 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
                       int activation, void *y, int y_dtype, int accumulate,
                       void *workspace, size_t workspace_bytes, void *stream);
 
+/* ---- routing from logits and the routed experts in one call: the topk, scan
+ *      and expert dispatches the reference encodes back to back into one command
+ *      buffer (encoder.rs:5275-5445) ----
+ * kr_moe_route(logits, tokens, experts, topk, normalize, selected, weights,
+ * counts, offsets, sorted_assign) followed by kr_q4_moe_experts(..., weights,
+ * offsets, sorted_assign, ...): the same arguments, limits, routing arrays and
+ * y bit for bit.  With one token on the routed GEMV path (KR_OPT_MOE_GEMV = 1)
+ * the routing runs inside the experts' first launch: every wavefront takes the
+ * token's softmax and top-k itself, one of them writes the routing arrays
+ * (KR_OPT_MOE_ROUTE_FUSED = 0 launches the routing kernel instead).  All checks
+ * of both stages run before anything is enqueued. */
+int kr_q4_moe_route_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down,
+                            uint32_t experts, const uint16_t *x, uint32_t tokens, uint32_t topk,
+                            const float *logits, int normalize, uint32_t *selected, float *weights,
+                            uint32_t *counts, uint32_t *offsets, uint32_t *sorted_assign,
+                            int activation, void *y, int y_dtype, int accumulate,
+                            void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- the whole routed MoE stage on the device: the SparseMoE channel mixer of
  *      forward_and_sample_impl / forward_prefill_batch (encoder.rs:5246-5445 and
  *      4425-4625): router Q4 GEMV -> top-k routing -> experts -> combine ----
  * logits = x . router^T in f32 (router: Q4 [experts, hidden]), then
- * kr_moe_route(logits, normalize) and kr_q4_moe_experts(...) as above, all on
+ * kr_q4_moe_route_experts(logits, normalize, ...) as above, all on
  * `stream` with nothing returned to the host.  The reference writes the router
  * logits as bf16 and reads them as f32, and never resets its expert counters
  * (encoder.rs:4435-4445, 5255-5265, 1982); here the logits stay f32 and the

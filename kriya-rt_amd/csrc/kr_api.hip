@@ -324,6 +324,14 @@ int kr_set_option(int option, int value) {
             if (value != 0 && value != 2 && value != 3) return fail(KR_E_INVALID, "few-token depth must be 0, 2 or 3");
             tuning().skinny_depth = value;
             return ok();
+        case KR_OPT_MOE_COMBINE:
+            if (value != 0 && value != 1) return fail(KR_E_INVALID, "moe combine must be 0 or 1");
+            tuning().moe_combine = value;
+            return ok();
+        case KR_OPT_MOE_ROUTE_FUSED:
+            if (value != 0 && value != 1) return fail(KR_E_INVALID, "moe route fused must be 0 or 1");
+            tuning().moe_route_fused = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -340,6 +348,8 @@ int kr_get_option(int option) {
         case KR_OPT_GEMV_LONG_ROWS: return tuning().gemv_long_rows;
         case KR_OPT_GEMV_TOKENS: return tuning().gemv_tokens;
         case KR_OPT_MOE_GEMV: return tuning().moe_gemv;
+        case KR_OPT_MOE_COMBINE: return tuning().moe_combine;
+        case KR_OPT_MOE_ROUTE_FUSED: return tuning().moe_route_fused;
         case KR_OPT_GEMV_LONG_GROUPS: return tuning().gemv_long_groups;
         case KR_OPT_SPLITK_TICKETS: return tuning().splitk_tickets;
         case KR_OPT_ATTN_MERGE_WAVE: return tuning().attn_merge_wave;
@@ -662,17 +672,34 @@ size_t kr_q4_moe_workspace_bytes(uint32_t tokens, uint32_t topk, uint32_t hidden
     return round_up(assign * inter * 2, 256) + round_up(assign * hidden * 4, 256);
 }
 
-int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, uint32_t experts,
-                      const uint16_t *x, uint32_t tokens, uint32_t topk, const float *weights, const uint32_t *offsets,
-                      const uint32_t *sorted_assign, int activation, void *y, int y_dtype, int accumulate,
-                      void *workspace, size_t workspace_bytes, void *stream) {
+namespace {
+// Routing computed inside the experts' first launch (kr_q4_moe_route_experts, one token).
+struct FusedRoute {
+    const float *logits;
+    int normalize;
+    uint32_t *selected, *counts;
+};
+
+// The routed GEMV path: few assignments, rows of <= 2048 columns.
+bool moe_gemv_path(uint32_t tokens, uint32_t topk, uint32_t hidden, uint32_t inter) {
+    return tuning().moe_gemv && (uint64_t)tokens * topk <= kMoeGemvMaxAssign && moe_gemv_fits(hidden) &&
+           moe_gemv_fits(inter);
+}
+
+// kr_q4_moe_experts' argument checks; hidden and inter on success.  tokens == 0 passes without the
+// pointer checks (the call then does nothing).
+int check_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, uint32_t experts,
+                      const uint16_t *x, uint32_t tokens, uint32_t topk, const float *weights,
+                      const uint32_t *offsets, const uint32_t *sorted_assign, int activation, void *y, int y_dtype,
+                      int accumulate, void *workspace, size_t workspace_bytes, uint32_t &hidden, uint32_t &inter) {
     if (int rc = check_matrix(gate, "gate")) return rc;
     if (int rc = check_matrix(up, "up")) return rc;
     if (int rc = check_matrix(down, "down")) return rc;
     if (experts == 0 || experts > kMaxExperts) return fail(KR_E_INVALID, "experts=%u must be in 1..%u", experts, kMaxExperts);
     if (gate->n != up->n || gate->k != up->k) return fail(KR_E_SHAPE, "gate and up shapes differ");
     if (gate->n % experts != 0) return fail(KR_E_SHAPE, "gate rows %u are not a multiple of experts=%u", gate->n, experts);
-    const uint32_t hidden = gate->k, inter = gate->n / experts;
+    hidden = gate->k;
+    inter = gate->n / experts;
     if (down->k != inter || down->n != experts * hidden)
         return fail(KR_E_SHAPE, "down [%u,%u] does not stack %u experts of [%u,%u]", down->n, down->k, experts, hidden,
                     inter);
@@ -684,7 +711,7 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
     if (!valid_dtype(y_dtype)) return fail(KR_E_INVALID, "y_dtype %d invalid", y_dtype);
     if (!valid_act(activation)) return fail(KR_E_INVALID, "activation %d invalid", activation);
     if (accumulate != 0 && accumulate != 1) return fail(KR_E_INVALID, "accumulate must be 0 or 1");
-    if (tokens == 0) return ok();
+    if (tokens == 0) return KR_OK;
     if ((uint64_t)tokens * topk > 0xFFFFFFFFull / 2) return fail(KR_E_SHAPE, "too many assignments");
     if (!x || !weights || !offsets || !sorted_assign || !y) return fail(KR_E_INVALID, "NULL pointer");
     if (!aligned(x, 16)) return fail(KR_E_ALIGN, "x must be 16-byte aligned");
@@ -695,12 +722,22 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
     if (!workspace || workspace_bytes < need)
         return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
     if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
+    return KR_OK;
+}
+
+// The experts after the checks: gate/up + activation, down, combine.  fr != nullptr (one token,
+// routed GEMV path): the gate/up launch routes the token and writes the routing arrays itself.
+int run_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, uint32_t experts,
+                    const uint16_t *x, uint32_t tokens, uint32_t topk, const float *weights,
+                    const uint32_t *offsets, const uint32_t *sorted_assign, int activation, void *y, int y_dtype,
+                    int accumulate, void *workspace, uint32_t hidden, uint32_t inter, void *stream,
+                    const FusedRoute *fr) {
     hipStream_t s = (hipStream_t)stream;
     const uint32_t assign = tokens * topk;
     uint16_t *h = (uint16_t *)workspace;                                              // [assign, inter] bf16, sorted order
     float *d = (float *)((char *)workspace + round_up((size_t)assign * inter * 2, 256));  // [assign, hidden] f32
 
-    if (tuning().moe_gemv && assign <= kMoeGemvMaxAssign && moe_gemv_fits(hidden) && moe_gemv_fits(inter)) {
+    if (moe_gemv_path(tokens, topk, hidden, inter)) {
         // few assignments: one m = 1 GEMV per (expert, token) pair, every expert row read once per assignment
         MoeGemvArgs g{};
         g.w = to_mat(gate);
@@ -715,6 +752,14 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
         g.out = h;
         g.ldo = inter;
         g.act = activation;
+        if (fr) {  // one token: the launch routes it and writes selected, weights, counts, offsets, sorted
+            g.logits = fr->logits;
+            g.normalize = fr->normalize;
+            g.topk = topk;
+            g.r_selected = fr->selected;
+            g.r_counts = fr->counts;
+            g.r_weights = const_cast<float *>(weights);
+        }
         if (hipError_t e = launch_moe_gemv(g, kGateUpBF16, s)) return hip_status(e, "kr_q4_moe_experts (gate/up)");
         MoeGemvArgs dn{};
         dn.w = dn.w2 = to_mat(down);
@@ -726,6 +771,23 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
         dn.assign = assign;
         dn.out = d;
         dn.ldo = hidden;
+        if (tuning().moe_combine && moe_down_combine_fits(inter, topk)) {
+            // the down projection sums the slots of each token itself: no d rows, no combine launch
+            MoeDownArgs dc{};
+            dc.w = to_mat(down);
+            dc.rows = hidden;
+            dc.h = h;
+            dc.offsets = offsets;
+            dc.sorted = sorted_assign;
+            dc.weights = weights;
+            dc.experts = experts;
+            dc.tokens = tokens;
+            dc.topk = topk;
+            dc.y = y;
+            dc.y_f32 = y_dtype == KR_DTYPE_F32;
+            dc.accumulate = accumulate;
+            return hip_status(launch_moe_down_combine(dc, s), "kr_q4_moe_experts (down + combine)");
+        }
         dn.out_scatter = 1;  // result rows back in assignment order
         if (hipError_t e = launch_moe_gemv(dn, kStoreF32, s)) return hip_status(e, "kr_q4_moe_experts (down)");
         return hip_status(launch_moe_combine(d, weights, tokens, topk, hidden, y, y_dtype == KR_DTYPE_F32, accumulate, s),
@@ -767,6 +829,55 @@ int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
 
     return hip_status(launch_moe_combine(d, weights, tokens, topk, hidden, y, y_dtype == KR_DTYPE_F32, accumulate, s),
                       "kr_q4_moe_experts (combine)");
+}
+}  // namespace
+
+int kr_q4_moe_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, uint32_t experts,
+                      const uint16_t *x, uint32_t tokens, uint32_t topk, const float *weights, const uint32_t *offsets,
+                      const uint32_t *sorted_assign, int activation, void *y, int y_dtype, int accumulate,
+                      void *workspace, size_t workspace_bytes, void *stream) {
+    uint32_t hidden = 0, inter = 0;
+    if (int rc = check_moe_experts(gate, up, down, experts, x, tokens, topk, weights, offsets, sorted_assign,
+                                   activation, y, y_dtype, accumulate, workspace, workspace_bytes, hidden, inter))
+        return rc;
+    if (tokens == 0) return ok();
+    return run_moe_experts(gate, up, down, experts, x, tokens, topk, weights, offsets, sorted_assign, activation, y,
+                           y_dtype, accumulate, workspace, hidden, inter, stream, nullptr);
+}
+
+int kr_q4_moe_route_experts(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down,
+                            uint32_t experts, const uint16_t *x, uint32_t tokens, uint32_t topk, const float *logits,
+                            int normalize, uint32_t *selected, float *weights, uint32_t *counts, uint32_t *offsets,
+                            uint32_t *sorted_assign, int activation, void *y, int y_dtype, int accumulate,
+                            void *workspace, size_t workspace_bytes, void *stream) {
+    // every check of both stages before the first launch: a failing call enqueues nothing
+    if (experts == 0 || experts > kMaxExperts) return fail(KR_E_INVALID, "experts=%u must be in 1..%u", experts, kMaxExperts);
+    if (topk == 0 || topk > experts || topk > kRouteMaxTopK)
+        return fail(KR_E_INVALID, "topk=%u must be in 1..min(experts, %u)", topk, kRouteMaxTopK);
+    if ((uint64_t)tokens * topk > kRouteMaxAssign)
+        return fail(KR_E_SHAPE, "tokens * topk = %llu exceeds %u", (unsigned long long)tokens * topk, kRouteMaxAssign);
+    if (!counts || !offsets) return fail(KR_E_INVALID, "counts/offsets must be non-NULL");
+    if (tokens > 0 && (!logits || !selected || !weights || !sorted_assign))
+        return fail(KR_E_INVALID, "logits/selected/weights/sorted_assign must be non-NULL");
+    if (!aligned(logits, 4) || !aligned(selected, 4) || !aligned(weights, 4) || !aligned(counts, 4) ||
+        !aligned(offsets, 4) || !aligned(sorted_assign, 4))
+        return fail(KR_E_ALIGN, "routing arrays must be 4-byte aligned");
+    uint32_t hidden = 0, inter = 0;
+    if (int rc = check_moe_experts(gate, up, down, experts, x, tokens, topk, weights, offsets, sorted_assign,
+                                   activation, y, y_dtype, accumulate, workspace, workspace_bytes, hidden, inter))
+        return rc;
+    if (tuning().moe_route_fused && tokens == 1 && moe_gemv_path(tokens, topk, hidden, inter) &&
+        moe_gemv_route_fits(experts, topk)) {
+        const FusedRoute fr{logits, normalize, selected, counts};
+        return run_moe_experts(gate, up, down, experts, x, tokens, topk, weights, offsets, sorted_assign, activation,
+                               y, y_dtype, accumulate, workspace, hidden, inter, stream, &fr);
+    }
+    if (int rc = kr_moe_route(logits, tokens, experts, topk, normalize, selected, weights, counts, offsets,
+                              sorted_assign, stream))
+        return rc;
+    if (tokens == 0) return ok();
+    return run_moe_experts(gate, up, down, experts, x, tokens, topk, weights, offsets, sorted_assign, activation, y,
+                           y_dtype, accumulate, workspace, hidden, inter, stream, nullptr);
 }
 
 // kr_q4_moe_block workspace: router logits f32 [T, E], selected u32 [T*K], weights f32 [T*K],
@@ -841,13 +952,11 @@ int kr_q4_moe_block(const kr_q4_matrix *router, const kr_q4_matrix *gate, const 
     uint32_t *sorted = (uint32_t *)(ws + L.sorted);
     // 1. router logits in f32 (the reference stores them as bf16 and reads them as f32)
     if (int rc = kr_q4_linear(router, x, tokens, logits, KR_DTYPE_F32, 0, stream)) return rc;
-    // 2. softmax, top-k, renormalisation, deterministic buckets
-    if (int rc = kr_moe_route(logits, tokens, experts, topk, normalize, selected, weights, counts, offsets, sorted,
-                              stream))
-        return rc;
-    // 3. experts (gate/up + activation, down) and the weighted combine into y
-    return kr_q4_moe_experts(gate, up, down, experts, x, tokens, topk, weights, offsets, sorted, activation, y, y_dtype,
-                             accumulate, ws + L.experts, L.total - L.experts, stream);
+    // 2. softmax, top-k, renormalisation, deterministic buckets; 3. experts (gate/up + activation,
+    // down) and the weighted combine into y
+    return kr_q4_moe_route_experts(gate, up, down, experts, x, tokens, topk, logits, normalize, selected, weights,
+                                   counts, offsets, sorted, activation, y, y_dtype, accumulate, ws + L.experts,
+                                   L.total - L.experts, stream);
 }
 
 int kr_q4_embedding(const kr_q4_matrix *w, const uint32_t *tokens, uint32_t count, uint16_t *out, void *stream) {

@@ -39,6 +39,10 @@ struct Tuning {
     int gemv_tokens = 1;               // 2 <= m <= 4: GEMV kernels over the tokens (1) or the few-token
                                        // MFMA kernel (0)
     int moe_gemv = 1;                  // MoE with <= 16 assignments: routed GEMV (1) or grouped MFMA kernel (0)
+    int moe_combine = 1;               // routed GEMV path, topk <= 4: combine folded into the down
+                                       // projection (1) or a launch of its own (0)
+    int moe_route_fused = 1;           // kr_q4_moe_route_experts with one token on the routed GEMV path:
+                                       // routing inside the gate/up launch (1) or a launch of its own (0)
     int splitk_tickets = 1;            // few-token split K: 1 the last block of a run reduces, 0 a second launch
     int attn_merge_wave = 1;           // decode attention merge of <= 64 slices, D a power of two 8..256:
                                        // 1 the barrier-free wave kernel, 0 the general block kernel
@@ -172,10 +176,34 @@ struct MoeGemvArgs {
     uint32_t ldo;
     int out_scatter, act;
     uint32_t tiles_per;         // set by the launcher
+    // One token routed inside the launch (logits != nullptr; gate/up only): every wave takes the
+    // token's softmax and top-k itself, and wave 0 of block 0 writes the routing arrays as the
+    // routing kernel does.  offsets/sorted above are then outputs, not inputs.
+    const float *logits;        // f32 [experts]
+    int normalize;
+    uint32_t topk;
+    uint32_t *r_selected, *r_counts;
+    float *r_weights;
 };
 constexpr uint32_t kMoeGemvMaxAssign = 16;  // the routed GEMV is used up to this many assignments
+// The routed down projection with the combine folded in (topk <= 4, rows of k <= 2048 columns).
+struct MoeDownArgs {
+    Q4Mat w;                    // stacked down matrices [experts * rows, k]
+    uint32_t rows;              // rows per expert (hidden)
+    const uint16_t *h;          // bf16 [assign, k], expert-sorted order
+    const uint32_t *offsets;    // [experts + 1]
+    const uint32_t *sorted;     // [assign]
+    const float *weights;       // [tokens * topk]
+    uint32_t experts, tokens, topk;
+    void *y;                    // [tokens, rows], f32 or bf16
+    int y_f32, accumulate;
+};
+bool moe_down_combine_fits(uint32_t k, uint32_t topk);
+hipError_t launch_moe_down_combine(const MoeDownArgs &a, hipStream_t s);
 bool moe_gemv_fits(uint32_t k);
 hipError_t launch_moe_gemv(MoeGemvArgs &a, int epilogue, hipStream_t s);
+// True when launch_moe_gemv can route the (single) token inside the gate/up launch.
+bool moe_gemv_route_fits(uint32_t experts, uint32_t topk);
 
 // ---- MoE routing and combine (moe.hip)
 constexpr uint32_t kRouteMaxTopK = 16;      // top-k list length of the routing kernel

@@ -31,6 +31,7 @@
 // FMAs:  acc += s * D + (b - 128 s) * sum(x).
 // Reductions run in a fixed order (transposing butterfly, then wave order),
 // so results are bitwise reproducible and independent of the grid size.
+#include "moe_route.hpp"
 #include "q4_dot2.hpp"
 
 namespace kr {
@@ -350,17 +351,85 @@ bool gemv_batch_supported(uint32_t k) { return k % 64 == 0 && k <= 2 * 64 * 32; 
 // Expert of p: the number of bucket ends offsets[1..E] <= p (one ballot per 64
 // experts).  The next item's words are requested before the current item is
 // reduced and stored, as in the wave kernel.
-template <int EPI>
+//
+// kRoute (one token, gate/up): the routing is part of the launch.  Every wave routes the token
+// itself (route_token_wave, the routing kernel's arithmetic, so the same experts and weights): the
+// K slots' experts e_k, and their positions p_k = #{k' : e_k' < e_k} + #{k' < k : e_k' == e_k} in
+// the expert-sorted order (offsets[e] + rank inside the bucket, as the routing kernel assigns
+// them).  Wave 0 of block 0 writes selected, weights, counts, offsets and sorted.
+template <int EPI, bool kRoute>
 __global__ __launch_bounds__(256) void q4_moe_gemv_kernel(MoeGemvArgs a) {
     constexpr int R = 2;
     constexpr bool kGateUp = (EPI == kGateUpF32 || EPI == kGateUpBF16);
     const int lane = threadIdx.x & (kWave - 1);
-    const uint32_t wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t wave = blockIdx.x * 4 + wid;
     const uint32_t nwaves = gridDim.x * 4;
     const uint32_t total = a.assign * a.tiles_per;
     const uint32_t per = (total + nwaves - 1) / nwaves;
     const uint32_t t_begin = wave * per, t_end = min(t_begin + per, total);
-    if (t_begin >= t_end) return;
+    uint32_t r_e = 0, r_p = 0;  // lane k < K: slot k's expert and sorted position (kRoute)
+    if constexpr (kRoute) {
+        // wave 0 of the block routes the token and hands (e_k, p_k) to the block's waves through LDS;
+        // wave 0 of block 0 also writes the routing arrays.  A block whose waves have no items
+        // (items go to waves in order) leaves at once, unless it is block 0.
+        __shared__ __attribute__((aligned(16))) float s_pr[kMaxExperts];
+        __shared__ __attribute__((aligned(16))) uint32_t s_ti[kRouteMaxTopK];
+        __shared__ uint32_t s_e[kRouteMaxTopK], s_p[kRouteMaxTopK];
+        __shared__ float s_tv[kRouteMaxTopK];
+        if (blockIdx.x * 4 * per >= total && blockIdx.x != 0) return;
+        if (wid == 0) {
+            float lv[kRoutePer];
+            load_logits(a.logits, a.experts, (uint32_t)lane, lv);
+            route_token_wave(lv, a.experts, a.topk, a.normalize, (uint32_t)lane, s_pr, s_ti, s_tv);
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const bool slot = (uint32_t)lane < a.topk;
+            uint32_t ek[kRouteMaxTopK];  // every slot's expert in every lane (16-byte LDS reads)
+#pragma unroll
+            for (uint32_t q = 0; q < kRouteMaxTopK / 4; ++q) {
+                const u32x4 v = reinterpret_cast<const u32x4 *>(s_ti)[q];
+                ek[4 * q] = v.x;
+                ek[4 * q + 1] = v.y;
+                ek[4 * q + 2] = v.z;
+                ek[4 * q + 3] = v.w;
+            }
+            r_e = s_ti[slot ? lane : 0];
+#pragma unroll
+            for (uint32_t k = 0; k < kRouteMaxTopK; ++k)
+                r_p += (k < a.topk && (ek[k] < r_e || (ek[k] == r_e && k < (uint32_t)lane))) ? 1u : 0u;
+            if (slot) {
+                s_e[lane] = r_e;
+                s_p[lane] = r_p;
+            }
+            if (blockIdx.x == 0) {
+                if (slot) {
+                    a.r_selected[lane] = r_e;
+                    a.r_weights[lane] = s_tv[lane];
+                    const_cast<uint32_t *>(a.sorted)[r_p] = (uint32_t)lane;
+                }
+                for (uint32_t e = (uint32_t)lane; e < a.experts; e += kWave) {
+                    uint32_t cnt = 0, below = 0;
+#pragma unroll
+                    for (uint32_t k = 0; k < kRouteMaxTopK; ++k) {
+                        cnt += (k < a.topk && ek[k] == e) ? 1u : 0u;
+                        below += (k < a.topk && ek[k] < e) ? 1u : 0u;
+                    }
+                    a.r_counts[e] = cnt;
+                    const_cast<uint32_t *>(a.offsets)[e] = below;
+                }
+                if (lane == 0) const_cast<uint32_t *>(a.offsets)[a.experts] = a.topk;
+            }
+        }
+        __syncthreads();
+        if (t_begin >= t_end) return;
+        const uint32_t k = (uint32_t)lane < a.topk ? (uint32_t)lane : 0u;
+        r_e = s_e[k];
+        r_p = s_p[k];
+    } else {
+        if (t_begin >= t_end) return;
+    }
     const uint32_t K = a.w.k, nchunks = K >> 5, wpr = K >> 3, groups = K >> 6;
     const uint32_t kMask = sgpr_const(0x000F000Fu);
     const uint32_t kMagic = vgpr_const(0x43004300u);
@@ -394,14 +463,22 @@ __global__ __launch_bounds__(256) void q4_moe_gemv_kernel(MoeGemvArgs a) {
     uint32_t X[16];
     uint32_t cur_p = 0xFFFFFFFFu, cur_xr = 0;
     auto enter = [&](uint32_t p) {
-        // sorted[p] through a lane-varying zero: a uniform load is moved to a scalar register
-        // right away (a wait before the expert lookup is even requested); this one stays in a
-        // vector register until its use
-        // Both are clamped: a position at or past offsets[E] (an id >= E that joined no bucket)
-        // has no expert and an unwritten sorted[p].  Its rows are then some expert's result for
-        // some assignment (unspecified), but every access stays inside the arrays.
-        const uint32_t sp = min(a.sorted[p + __builtin_amdgcn_mbcnt_lo(0u, 0u)], a.assign - 1);
-        const uint32_t e = min(expert_of(p), a.experts - 1);
+        uint32_t sp, e;
+        if constexpr (kRoute) {
+            // the slot at position p (positions of the K slots are distinct, 0 .. K-1)
+            const uint64_t m = __ballot((uint32_t)lane < a.topk && r_p == p);
+            sp = m ? (uint32_t)__builtin_ctzll(m) : 0u;
+            e = min(__builtin_amdgcn_readlane(r_e, sp), a.experts - 1);
+        } else {
+            // sorted[p] through a lane-varying zero: a uniform load is moved to a scalar register
+            // right away (a wait before the expert lookup is even requested); this one stays in a
+            // vector register until its use
+            // Both are clamped: a position at or past offsets[E] (an id >= E that joined no bucket)
+            // has no expert and an unwritten sorted[p].  Its rows are then some expert's result for
+            // some assignment (unspecified), but every access stays inside the arrays.
+            sp = min(a.sorted[p + __builtin_amdgcn_mbcnt_lo(0u, 0u)], a.assign - 1);
+            e = min(expert_of(p), a.experts - 1);
+        }
         const size_t r0 = (size_t)e * a.rows;
         A.qw = a.w.qw + r0 * wpr;
         A.sc = a.w.sc + r0 * groups;
@@ -467,20 +544,188 @@ __global__ __launch_bounds__(256) void q4_moe_gemv_kernel(MoeGemvArgs a) {
     }
 }
 
+// The routed down projection with the combine folded in (few assignments, topk <= 4; replaces the
+// down GEMV + moe_combine_kernel pair, transformer_glue.metal:373-401).  Items are (token t, row
+// pair i), token-major; wave w takes the contiguous run [w * per, (w + 1) * per).  For every slot
+// k < KS of t (slots >= topk repeat the last one and are not summed) the slot's position p_k in the
+// expert-sorted list (the lane j < assign holding sorted[j] == t * topk + k) and its expert e_k
+// (bucket ends <= p_k) select rows e_k * rows + 2i, 2i + 1 of the stacked matrices and h row p_k.
+// The 2 * KS dots are reduced at once on the fixed tree, on which each value is summed exactly as
+// the two-row reduction of the routed GEMV sums it, so every d_k has the bits of the down GEMV's f32
+// output; then y[t, row] (+)= sum_k fma(w[t, k], d_k, acc) in slot order, moe_combine_kernel's
+// arithmetic.  The results are those of the three-launch path bit for bit.
+template <int KS>
+__global__ __launch_bounds__(256) void q4_moe_down_combine_kernel(MoeDownArgs a) {
+    constexpr int R = 2, NV = R * KS, kSeg = kWave / NV;
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t nwaves = gridDim.x * 4;
+    const uint32_t tiles = (a.rows + 1) / 2;
+    const uint32_t total = a.tokens * tiles;
+    const uint32_t per = (total + nwaves - 1) / nwaves;
+    const uint32_t t_begin = wave * per, t_end = min(t_begin + per, total);
+    if (t_begin >= t_end) return;
+    const uint32_t K = a.w.k, nchunks = K >> 5, wpr = K >> 3, groups = K >> 6;
+    const uint32_t kMask = sgpr_const(0x000F000Fu);
+    const uint32_t kMagic = vgpr_const(0x43004300u);
+    const uint32_t kSelLo = sgpr_const(0x05040100u);
+    const uint32_t kSelHi = sgpr_const(0x07060302u);
+    const bool live = (uint32_t)lane < nchunks;
+    const uint32_t c = live ? (uint32_t)lane : 0u;
+    const uint32_t assign = a.tokens * a.topk;
+    // the routing state, requested once: lane j < assign holds sorted[j], lane j of round i the bucket
+    // end offsets[64 i + j + 1] (unrolled with uniform guards and clamped loads: no loop waits)
+    const uint32_t srt = a.sorted[min((uint32_t)lane, assign - 1)];
+    uint32_t ends[kMaxExperts / kWave];
+#pragma unroll
+    for (uint32_t i = 0; i < kMaxExperts / kWave; ++i)
+        ends[i] = i * kWave < a.experts ? a.offsets[min(i * kWave + (uint32_t)lane, a.experts - 1) + 1] : 0u;
+
+    uint32_t xrow[KS];
+    size_t rbase[KS];
+    float wk[KS];
+    uint32_t cur_t = 0xFFFFFFFFu;
+    auto enter = [&](uint32_t tok) {
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const uint32_t aid = tok * a.topk + min((uint32_t)k, a.topk - 1);
+            const uint64_t m = __ballot((uint32_t)lane < assign && srt == aid);
+            // an assignment that joined no bucket (expert id >= E) has no position: its rows are some
+            // expert's (unspecified), every access in bounds
+            const uint32_t p = m ? (uint32_t)__builtin_ctzll(m) : 0u;
+            uint32_t e = 0;
+#pragma unroll
+            for (uint32_t i = 0; i < kMaxExperts / kWave; ++i) {
+                if (i * kWave < a.experts) {
+                    const uint32_t j = i * kWave + (uint32_t)lane;
+                    e += (uint32_t)__popcll(__ballot(j < a.experts && ends[i] <= p));
+                }
+            }
+            e = min(e, a.experts - 1);
+            xrow[k] = p;
+            rbase[k] = (size_t)e * a.rows;
+            wk[k] = a.weights[aid];
+        }
+        cur_t = tok;
+    };
+
+    u32x4 wv[KS][R];
+    uint32_t sv[KS][R], bv[KS][R];
+    auto fetch = [&](uint32_t i) {
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const size_t row = rbase[k] + min(2 * i + (uint32_t)r, a.rows - 1);  // a tail row is never stored
+                wv[k][r] = ld_stream(reinterpret_cast<const u32x4 *>(a.w.qw + row * wpr) + c);
+                sv[k][r] = ld_stream(a.w.sc + row * groups + (c >> 1));
+                bv[k][r] = ld_stream(a.w.bi + row * groups + (c >> 1));
+            }
+        }
+    };
+    uint32_t X[KS][16];
+    XChunk xc[KS];
+    auto load_x = [&] {
+#pragma unroll
+        for (int k = 0; k < KS; ++k) load_xwords(X[k], a.h + (size_t)xrow[k] * K, c);
+    };
+    uint32_t t = t_begin;
+    enter(t / tiles);
+    fetch(t % tiles);
+    load_x();
+    bool x_new = true;
+    for (;;) {
+        if (x_new) {
+#pragma unroll
+            for (int k = 0; k < KS; ++k) build_xchunk(xc[k], X[k], kSelLo, kSelHi);
+        }
+        x_new = false;
+        float acc[NV];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const float d = chunk_dot(wv[k][r], sv[k][r], bv[k][r], xc[k], 0.0f, kMask, kMagic);
+                acc[k * R + r] = live ? d : 0.0f;
+            }
+        }
+        const uint32_t i = t % tiles, tok = cur_t;
+        float w[KS];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) w[k] = wk[k];
+        const uint32_t tn = t + 1;
+        if (tn < t_end) {
+            if (tn / tiles != cur_t) {
+                enter(tn / tiles);
+                fetch(tn % tiles);
+                load_x();
+                x_new = true;
+            } else {
+                fetch(tn % tiles);
+            }
+        }
+        const float tot = wave_reduce_rows<NV>(acc, lane);  // segment v = k * R + r holds d_k of row r
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float y = 0.0f;
+#pragma unroll
+            for (int k = 0; k < KS; ++k) {
+                const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), (k * R + r) * kSeg));
+                if ((uint32_t)k < a.topk) y = fmaf(w[k], d, y);
+            }
+            const uint32_t row = 2 * i + r;
+            if (lane == r && row < a.rows) {
+                const size_t o = (size_t)tok * a.rows + row;
+                if (a.y_f32) {
+                    float *out = reinterpret_cast<float *>(a.y) + o;
+                    *out = a.accumulate ? *out + y : y;
+                } else {
+                    uint16_t *out = reinterpret_cast<uint16_t *>(a.y) + o;
+                    *out = (uint16_t)f32_to_bf16(a.accumulate ? bf16_to_f32(*out) + y : y);
+                }
+            }
+        }
+        if (tn >= t_end) break;
+        t = tn;
+    }
+}
+
 bool moe_gemv_fits(uint32_t k) { return k % 64 == 0 && k <= 2048; }
+bool moe_gemv_route_fits(uint32_t experts, uint32_t topk) {
+    return experts >= 1 && experts <= kMaxExperts && topk >= 1 && topk <= kRouteMaxTopK && topk <= experts;
+}
 
 hipError_t launch_moe_gemv(MoeGemvArgs &a, int epilogue, hipStream_t s) {
     if (!moe_gemv_fits(a.w.k) || a.assign == 0) return hipErrorInvalidValue;
     const bool gate_up = epilogue == kGateUpBF16 || epilogue == kGateUpF32;
+    if (a.logits && (!gate_up || a.assign != a.topk || !moe_gemv_route_fits(a.experts, a.topk)))
+        return hipErrorInvalidValue;  // in-launch routing: one token, gate/up
     a.tiles_per = gate_up ? a.rows : (a.rows + 1) / 2;  // two rows per tile: (gate, up) or a row pair
     const uint32_t total = a.assign * a.tiles_per;
     const uint32_t blocks = cap_blocks((total + 3) / 4, (uint32_t)tuning().gemv_persistent_blocks);
     switch (epilogue) {
         case kGateUpBF16:
-            hipLaunchKernelGGL((q4_moe_gemv_kernel<kGateUpBF16>), dim3(blocks), dim3(256), 0, s, a);
+            if (a.logits) hipLaunchKernelGGL((q4_moe_gemv_kernel<kGateUpBF16, true>), dim3(blocks), dim3(256), 0, s, a);
+            else hipLaunchKernelGGL((q4_moe_gemv_kernel<kGateUpBF16, false>), dim3(blocks), dim3(256), 0, s, a);
             break;
-        case kStoreF32: hipLaunchKernelGGL((q4_moe_gemv_kernel<kStoreF32>), dim3(blocks), dim3(256), 0, s, a); break;
+        case kStoreF32:
+            hipLaunchKernelGGL((q4_moe_gemv_kernel<kStoreF32, false>), dim3(blocks), dim3(256), 0, s, a);
+            break;
         default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+bool moe_down_combine_fits(uint32_t k, uint32_t topk) { return moe_gemv_fits(k) && topk >= 1 && topk <= 4; }
+
+hipError_t launch_moe_down_combine(const MoeDownArgs &a, hipStream_t s) {
+    if (!moe_down_combine_fits(a.w.k, a.topk) || a.tokens == 0 || a.rows == 0) return hipErrorInvalidValue;
+    const uint32_t total = a.tokens * ((a.rows + 1) / 2);
+    const uint32_t blocks = cap_blocks((total + 3) / 4, (uint32_t)tuning().gemv_persistent_blocks);
+    switch (a.topk) {
+        case 1: hipLaunchKernelGGL((q4_moe_down_combine_kernel<1>), dim3(blocks), dim3(256), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((q4_moe_down_combine_kernel<2>), dim3(blocks), dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL((q4_moe_down_combine_kernel<4>), dim3(blocks), dim3(256), 0, s, a); break;
     }
     return hipGetLastError();
 }

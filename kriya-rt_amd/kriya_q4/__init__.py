@@ -38,6 +38,8 @@ OPT_ATTN_MERGE_WAVE = 13
 OPT_PREFILL_OPERANDS = 14
 OPT_SKINNY_GROUPS = 15
 OPT_SKINNY_DEPTH = 16
+OPT_MOE_COMBINE = 17
+OPT_MOE_ROUTE_FUSED = 18
 
 _lib = None
 
@@ -90,6 +92,8 @@ def lib():
             "kr_moe_scan_scatter": (i32, [vp, u32, u32, vp, vp, vp, vp]),
             "kr_q4_moe_workspace_bytes": (sz, [u32, u32, u32, u32]),
             "kr_q4_moe_experts": (i32, [M, M, M, u32, vp, u32, u32, vp, vp, vp, i32, vp, i32, i32, vp, sz, vp]),
+            "kr_q4_moe_route_experts": (i32, [M, M, M, u32, vp, u32, u32, vp, i32, vp, vp, vp, vp, vp, i32, vp, i32,
+                                              i32, vp, sz, vp]),
             "kr_q4_moe_block_workspace_bytes": (sz, [u32, u32, u32, u32, u32]),
             "kr_q4_moe_block": (i32, [M, M, M, M, u32, vp, u32, u32, i32, i32, vp, i32, i32, vp, sz, vp]),
             "kr_q4_embedding": (i32, [M, vp, u32, vp, vp]),
@@ -380,6 +384,25 @@ def moe_experts(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, experts: int, x: t
                                    _ptr(y), _dt_of(y), int(accumulate), _ptr(workspace), workspace.numel(),
                                    _stream(stream)))
     return y
+
+
+def moe_route_experts(gate: Q4Matrix, up: Q4Matrix, down: Q4Matrix, experts: int, x: torch.Tensor,
+                      logits: torch.Tensor, topk: int, normalize: bool = True, out: Optional[MoeRoute] = None,
+                      y: Optional[torch.Tensor] = None, out_dtype: int = DTYPE_F32, accumulate: bool = False,
+                      activation: int = ACT_SWIGLU, workspace: Optional[torch.Tensor] = None, stream=None):
+    """moe_route(logits) then moe_experts in one call (kr_q4_moe_route_experts); returns (y, route)."""
+    tokens = int(logits.shape[0])
+    if out is None:
+        out = MoeRoute(tokens, experts, topk, device=logits.device)
+    if y is None:
+        y = torch.zeros((tokens, gate.k), dtype=_out_dtype(out_dtype), device=x.device)
+    if workspace is None:
+        workspace = moe_workspace(tokens, topk, gate.k, gate.n // experts, device=x.device)
+    _check(lib().kr_q4_moe_route_experts(gate.desc, up.desc, down.desc, experts, _ptr(x), tokens, topk, _ptr(logits),
+                                         int(normalize), _ptr(out.selected), _ptr(out.weights), _ptr(out.counts),
+                                         _ptr(out.offsets), _ptr(out.sorted_assign), activation, _ptr(y), _dt_of(y),
+                                         int(accumulate), _ptr(workspace), workspace.numel(), _stream(stream)))
+    return y, out
 
 
 def moe_block_workspace(tokens: int, experts: int, topk: int, hidden: int, inter: int, device="cuda") -> torch.Tensor:

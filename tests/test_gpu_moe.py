@@ -296,3 +296,78 @@ def test_moe_deterministic_and_graph_replay(kq):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, ref)
+
+
+@pytest.mark.parametrize("T,E,K,hidden,inter", [(1, 60, 4, 2048, 1408), (2, 8, 2, 256, 128), (4, 6, 3, 512, 384),
+                                                (16, 8, 1, 512, 384), (3, 5, 4, 128, 1024), (1, 16, 2, 2048, 2048)])
+def test_moe_combine_folded_into_down_bitwise(kq, T, E, K, hidden, inter):
+    """Few assignments with topk <= 4: the routed down projection sums each token's slots itself
+    (KR_OPT_MOE_COMBINE = 1, the default) -- the bits of the down GEMV followed by the combine launch
+    (option 0) for f32 and bf16 outputs, plain and accumulated, and within the bar of the oracle."""
+    case(f"moe combine folded into down T={T} E={E} K={K} hidden={hidden} inter={inter}")
+    g, u, d, x, logits, route, want = moe_case(kq, T, E, K, hidden, inter, 4800 + 7 * T + E + K)
+    r = route_from_oracle(kq, *route, T, E, K)
+    gd, ud, dd = q4_dev(kq, g), q4_dev(kq, u), q4_dev(kq, d)
+    r0 = synth().bf16_normal((T, hidden), 4899)
+    outs = {}
+    try:
+        for opt in (0, 1):
+            kq.set_option(kq.OPT_MOE_COMBINE, opt)
+            yf = kq.moe_experts(gd, ud, dd, E, dev_bf16(x), r)
+            yb = kq.moe_experts(gd, ud, dd, E, dev_bf16(x), r, out_dtype=kq.DTYPE_BF16)
+            accf = torch.from_numpy(O.bf16_to_f32(r0)).cuda()
+            kq.moe_experts(gd, ud, dd, E, dev_bf16(x), r, y=accf, accumulate=True)
+            accb = dev_bf16(r0).clone()
+            kq.moe_experts(gd, ud, dd, E, dev_bf16(x), r, y=accb, accumulate=True)
+            outs[opt] = [t.view(torch.int16 if t.dtype == torch.bfloat16 else torch.int32).cpu().numpy()
+                         for t in (yf, yb, accf, accb)]
+    finally:
+        kq.set_option(kq.OPT_MOE_COMBINE, 1)
+    for i, name in enumerate(("f32", "bf16", "acc f32", "acc bf16")):
+        assert np.array_equal(outs[0][i], outs[1][i]), name
+    assert_rms_close(outs[1][0].view(np.float32), want, what="folded combine f32")
+
+
+@pytest.mark.parametrize("E,K,hidden,inter,kind", [(60, 4, 2048, 1408, "normal"), (16, 2, 512, 384, "normal"),
+                                                   (8, 8, 256, 128, "normal"), (256, 16, 128, 128, "normal"),
+                                                   (12, 4, 256, 128, "ties"), (12, 6, 256, 128, "nan")])
+def test_moe_route_experts_one_token_bitwise(kq, E, K, hidden, inter, kind):
+    """kr_q4_moe_route_experts with one token routes inside the gate/up launch (KR_OPT_MOE_ROUTE_FUSED = 1):
+    the routing arrays and y are those of the routing kernel followed by kr_q4_moe_experts (option 0) bit for
+    bit -- also with tied logits (ties go to the lower id) and with NaN logits (never taken; slots left
+    empty hold expert 0 with weight -inf) -- and the routing is the oracle's."""
+    s = synth()
+    case(f"moe route+experts one token, E={E} K={K} hidden={hidden} inter={inter} {kind}")
+    g, u, d = s.q4_weight(E * inter, hidden, 4901), s.q4_weight(E * inter, hidden, 4902), s.q4_weight(E * hidden, inter, 4903)
+    gd, ud, dd = q4_dev(kq, g), q4_dev(kq, u), q4_dev(kq, d)
+    x = dev_bf16(s.bf16_normal((1, hidden), 4904))
+    logits = s.f32_normal((1, E), 4905).astype(np.float32)
+    if kind == "ties":
+        logits[0, 1::3] = logits[0, 0]  # every third expert ties with expert 0
+    if kind == "nan":
+        logits[0, : E - 3] = np.nan  # only three finite logits for K = 6 slots
+    lt = torch.from_numpy(logits).cuda()
+    res = {}
+    try:
+        for opt in (0, 1):
+            kq.set_option(kq.OPT_MOE_ROUTE_FUSED, opt)
+            r = kq.MoeRoute(1, E, K)
+            for t in (r.selected, r.counts, r.offsets, r.sorted_assign):
+                t.fill_(-1)
+            r.weights.fill_(7.0)
+            y, _ = kq.moe_route_experts(gd, ud, dd, E, x, lt, K, out=r)
+            res[opt] = [t.view(torch.int32).cpu().numpy() for t in (r.selected, r.weights, r.counts, r.offsets,
+                                                                    r.sorted_assign, y)]
+    finally:
+        kq.set_option(kq.OPT_MOE_ROUTE_FUSED, 1)
+    for i, name in enumerate(("selected", "weights", "counts", "offsets", "sorted", "y")):
+        assert np.array_equal(res[0][i], res[1][i]), name
+    want_sel, want_w, want_cnt, want_off, want_sorted = O.moe_route(logits, K, True)
+    assert np.array_equal(res[1][0].ravel().astype(np.uint32), np.asarray(want_sel, np.uint32).ravel())
+    assert np.array_equal(res[1][2].astype(np.uint32), np.asarray(want_cnt, np.uint32))
+    assert np.array_equal(res[1][3].astype(np.uint32), np.asarray(want_off, np.uint32))
+    assert np.array_equal(res[1][4].astype(np.uint32), np.asarray(want_sorted, np.uint32))
+    if kind != "nan":
+        want = O.moe_experts(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), E, s.bf16_normal((1, hidden), 4904),
+                             want_sel, want_w)
+        assert_rms_close(res[1][5].view(np.float32), want, what="route+experts")
