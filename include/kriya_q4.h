@@ -127,6 +127,10 @@ const char *kr_last_error(void);
 #define KR_OPT_MOE_ROUTE_FUSED 18      /* kr_q4_moe_route_experts / kr_q4_moe_block with one token on the
                                          * routed GEMV path: 1 (default) the routing runs inside the gate/up
                                          * launch; 0 the routing kernel first.  Bitwise the same. */
+#define KR_OPT_PREFILL_XCD_SPLIT 19     /* prefill kernel with K split over blocks (kr_q4_mlp's down
+                                         * projection at m >= 64): 1 (default) the blocks of each K split
+                                         * are placed on their own XCDs, so that an L2 holds one K range
+                                         * of x; 0 the tile grouping of unsplit launches.  Bitwise the same. */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 

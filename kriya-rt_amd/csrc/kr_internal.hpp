@@ -44,6 +44,8 @@ struct Tuning {
     int moe_route_fused = 1;           // kr_q4_moe_route_experts with one token on the routed GEMV path:
                                        // routing inside the gate/up launch (1) or a launch of its own (0)
     int splitk_tickets = 1;            // few-token split K: 1 the last block of a run reduces, 0 a second launch
+    int prefill_xcd_split = 1;         // prefill split K: each K split on its own XCDs (1) or the tile
+                                       // grouping of unsplit launches (0)
     int attn_merge_wave = 1;           // decode attention merge of <= 64 slices, D a power of two 8..256:
                                        // 1 the barrier-free wave kernel, 0 the general block kernel
     int prefill_operands = 1;          // kr_q4_mlp at m >= 64: 1 fp16 operands converted once per call
@@ -98,6 +100,9 @@ struct MfmaArgs {
     // prefill gate/up with bf16 output only: also write the output converted the same way (the
     // next projection's xh), [m, ldo] fp16
     uint16_t *out_h;
+    // prefill split K, set by the launcher: > 0 places each K split on 8 / ksplit XCDs, each taking
+    // `xcd_tiles` consecutive tiles (see q4_prefill_kernel); 0 the default tile grouping
+    uint32_t xcd_tiles;
 };
 
 // bm: the M tile class (16, 64 or 128) chosen by the caller from m.

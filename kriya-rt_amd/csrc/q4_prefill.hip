@@ -161,10 +161,21 @@ __global__ __launch_bounds__(64 * WAVES * KW, OCC) void q4_prefill_kernel(MfmaAr
     const int c = lane & 15, kq = lane >> 4;
     char *const xring = lds + kg * (D + 1) * kBuf;  // this group's X buffers
 
-    // ---- block -> (problem, n tile, m tile); the M tiles of one N tile share an XCD
+    // ---- block -> (problem, n tile, m tile, K split).  Workgroups go to the 8 XCDs (each with its own
+    // L2) round-robin in launch order.  Unsplit: the M tiles of one N tile share an XCD, so each
+    // weight tile is read into one L2.  Split K (xcd_tiles > 0, one problem): the blocks of K split
+    // ks go to XCDs ks * 8 / ksplit ..; XCD j takes the xcd_tiles consecutive tiles (whole N tiles
+    // with all their M tiles) of part j % (8 / ksplit), so an L2 holds one K range of X and of the
+    // weights instead of all of X.  Any grid maps one-to-one; only locality depends on the order.
     const uint32_t nblk = gridDim.x;
-    uint32_t bid = blockIdx.x;
-    if (nblk >= 8 && (nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    uint32_t bid = blockIdx.x, ks = blockIdx.y;
+    if (args.xcd_tiles) {
+        const uint32_t L = blockIdx.x + blockIdx.y * nblk, j = L & 7, g = 8 / gridDim.y;
+        ks = j / g;
+        bid = (j % g) * args.xcd_tiles + (L >> 3);
+    } else if (nblk >= 8 && (nblk & 7) == 0) {
+        bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    }
     int pi = 0;
 #pragma unroll
     for (int i = 1; i < kMaxMfmaProblems; ++i)
@@ -177,7 +188,6 @@ __global__ __launch_bounds__(64 * WAVES * KW, OCC) void q4_prefill_kernel(MfmaAr
     const uint32_t N = P.w.n, M = args.m, K = args.k, G = K >> 6;
     const uint32_t GS = G / SW;                                // steps over the whole row
     const uint32_t row0 = nt * T::kBN + wave * T::kWaveRows;  // first weight row of this wave
-    const uint32_t ks = blockIdx.y;
     const uint32_t g_begin = ks * (args.groups_per_split / SW);  // in steps (groups_per_split % SW == 0)
     const uint32_t g_end = min(GS, g_begin + args.groups_per_split / SW);
 
@@ -736,6 +746,11 @@ static hipError_t launch_prefill_shape(MfmaArgs &a, hipStream_t s) {
     if (a.ksplit <= 1) a.groups_per_split = a.k / 64;
     if (a.groups_per_split % SW != 0) return hipErrorInvalidValue;
     const dim3 grid(tiles, a.ksplit > 1 ? a.ksplit : 1);
+    // split K over XCDs (q4_prefill_kernel): one problem, 8 % ksplit == 0 and whole tile ranges per XCD
+    a.xcd_tiles = 0;
+    if (tuning().prefill_xcd_split && a.np == 1 && (a.ksplit == 2 || a.ksplit == 4 || a.ksplit == 8) &&
+        tiles % (8 / a.ksplit) == 0)
+        a.xcd_tiles = tiles / (8 / a.ksplit);
     if (a.ksplit > 1) {
         hipLaunchKernelGGL((q4_prefill_kernel<MF, NF, WAVES, NW, OCC, kMfmaPartial, D, SW, KW>), grid, dim3(T::kThreads),
                            kLdsPartial, s, a);

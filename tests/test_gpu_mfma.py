@@ -454,3 +454,30 @@ def test_prefill_fp16_overflow_fallback_k2048(kq, opt):
                 assert_rms_close(got[i], want[i], what=f"{name} row {i}")
     finally:
         lib.kr_set_option(kq.OPT_PREFILL_KERNEL, 0)
+
+
+@pytest.mark.parametrize("m,hidden,inter", [(512, 2048, 11008), (96, 512, 1408), (200, 1024, 2816)])
+def test_prefill_xcd_split_bitwise(kq, m, hidden, inter):
+    """kr_q4_mlp's split-K down projection places each K split on its own XCDs (KR_OPT_PREFILL_XCD_SPLIT = 1,
+    the default): a different block order over the same (tile, split) pairs, so the same bits as the default
+    tile grouping (option 0), and within the bar of the oracle."""
+    s = synth()
+    case(f"prefill split K on per-split XCDs, mlp m={m} hidden={hidden} inter={inter}")
+    g, u, d = s.q4_weight(inter, hidden, 2901), s.q4_weight(inter, hidden, 2902), s.q4_weight(hidden, inter, 2903)
+    G, U, D = (q4_dev(kq, t) for t in (g, u, d))
+    x = s.bf16_normal((m, hidden), 2904)
+    ws = kq.mlp_workspace(m, hidden, inter)
+    res = {}
+    try:
+        for opt in (0, 1):
+            kq.set_option(kq.OPT_PREFILL_XCD_SPLIT, opt)
+            h = torch.zeros((m, hidden), dtype=torch.float32, device="cuda")
+            kq.mlp(G, U, D, h, x=dev_bf16(x), workspace=ws)
+            res[opt] = h.cpu().numpy()
+    finally:
+        kq.set_option(kq.OPT_PREFILL_XCD_SPLIT, 1)
+    assert np.array_equal(res[0].view(np.uint32), res[1].view(np.uint32))
+    if m <= 200:
+        want = O.q4_mlp(O.Q4Planar(*g), O.Q4Planar(*u), O.Q4Planar(*d), x)
+        for i in range(m):
+            assert_rms_close(res[1][i], want[i], what=f"row {i}")
