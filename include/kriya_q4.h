@@ -131,6 +131,11 @@ const char *kr_last_error(void);
                                          * projection at m >= 64): 1 (default) the blocks of each K split
                                          * are placed on their own XCDs, so that an L2 holds one K range
                                          * of x; 0 the tile grouping of unsplit launches.  Bitwise the same. */
+#define KR_OPT_ATTN_SLICE64 20          /* kr_rope_attention_decode with head_dim 128: slices of 64 positions
+                                         * (one wave per 16 of them, all dims) instead of 16 (four waves
+                                         * over the dims): 1 (default) when batch * kv_heads * slices still
+                                         * gives one block per compute unit, 2 always, 0 never.  The f32
+                                         * sums differ in order. */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 

@@ -503,6 +503,229 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
     }
 }
 
+// attention_split64_kernel: the split kernel's job for head_dim 128 on slices of 64 positions.
+// Grid (ceil(max_ctx / 64), kv_heads, batch), 256 threads: wave w takes positions p0 + 16 w ..
+// p0 + 16 w + 15 of the block's slice for all G <= 16 query heads of the kv head, with every
+// dimension (no partial tiles to add across waves):
+//   0. loads first: its key pieces in the matrix-core layout (position p0 + 16 w + l % 16, dims
+//      32 s + 8 (l / 16), s < 4) and value pieces (position p0 + 16 w + l / 16 + 4 m, dims
+//      8 (l % 16)), the query pairs, the RoPE row of the new position, the new k and v;
+//   1. the G query heads rotated (bf16-rounded, as kr_rope_kv_append stores them) into LDS, and
+//      the new key if the slice holds the new position (its own scores take it from LDS);
+//   2. scores: four v_mfma_f32_16x16x32_bf16 (query rows x key columns; bf16 products are exact,
+//      sums f32), scaled by 1/sqrt(128), -inf past the sequence;
+//   3. per head the wave's max m over its 16 positions, p = e^(s - m), the sum l;
+//   4. values: the probabilities (bf16 hi + lo, P = hi + lo to 2^-17; transposed through the
+//      wave's LDS tile) times the value tile on v_mfma_f32_16x16x16_bf16, both products exact;
+//   5. the 4 waves' (m, l, acc) merged in wave order into the slice's partial
+//        m = max_w m_w,  l = sum_w e^(m_w - m) l_w,  acc = sum_w e^(m_w - m) acc_w,
+//      the layout the merge kernels read (a slice past the sequence publishes (-inf, 0) only).
+// Against 16-position slices: a quarter of the blocks, of the query rotations and of the
+// partials the merge reads.
+constexpr uint32_t kSplit64 = 64;
+
+__global__ __launch_bounds__(256) void attention_split64_kernel(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                                                const float *cos_sin, const uint32_t *positions,
+                                                                uint32_t q_heads, uint32_t kv_heads, uint16_t *k_cache,
+                                                                uint16_t *v_cache, uint32_t max_ctx, float *part) {
+    constexpr uint32_t D = 128, half = 64;
+    constexpr uint32_t QS = D + 8;  // query / value tile row stride: the rows one 16-byte (or B-fragment)
+    constexpr uint32_t VS = D + 8;  // read takes sit 4 (16) banks apart
+    constexpr uint32_t AS = D + 4;  // merge rows: the 4 head groups of a write 16 banks apart
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    __shared__ __align__(16) uint16_t qs[16 * QS];           // rotated queries, bf16 [head][dim]
+    __shared__ __align__(16) uint16_t knew[D], vnew[D];      // the new key (rotated) and value
+    __shared__ __align__(16) uint16_t vt[4][16 * VS];        // per-wave value tile [position][dim]
+    __shared__ __align__(16) float pt[4][16 * 16];           // per-wave probability tile [head][position]
+    __shared__ float mrow[4][16], lrow[4][16];
+    __shared__ __align__(16) float accm[4][16 * AS];         // per-wave unnormalised outputs [head][dim]
+    const uint32_t tid = threadIdx.x, l = tid & 63, row = l & 15, kq = l >> 4;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, splits = gridDim.x;
+    const uint32_t G = q_heads / kv_heads;
+    const uint32_t pos = __builtin_amdgcn_readfirstlane(positions[b]);
+    const bool append = pos < max_ctx;
+    const uint32_t n = min(pos, max_ctx - 1) + 1;  // positions attended
+    const uint32_t s0 = s * kSplit64, p0 = s0 + 16 * w;
+    float *out = part + (((size_t)b * kv_heads + kvh) * splits + s) * (size_t)G * (D + 2);  // m[G], l[G], acc[G][D]
+    if (s0 >= n) {  // nothing of this sequence in the slice
+        if (tid < G) {
+            out[tid] = -INFINITY;
+            out[G + tid] = 0.0f;
+        }
+        return;
+    }
+    const bool has_new = append && pos >= s0 && pos < s0 + kSplit64;
+    const size_t rs = (size_t)kv_heads * D;
+    const uint16_t *kb = k_cache + ((size_t)b * max_ctx * kv_heads + kvh) * D;
+    const uint16_t *vb = v_cache + ((size_t)b * max_ctx * kv_heads + kvh) * D;
+    // 0. loads (clamped rows; what must not contribute is masked or zeroed at use)
+    u32x4 kw[4], vw[4];
+    {
+        const uint32_t kp = min(p0 + row, max_ctx - 1);
+#pragma unroll
+        for (uint32_t s2 = 0; s2 < 4; ++s2) kw[s2] = *reinterpret_cast<const u32x4 *>(kb + kp * rs + 32 * s2 + 8 * kq);
+#pragma unroll
+        for (uint32_t m = 0; m < 4; ++m) {
+            const uint32_t vp = min(p0 + kq + 4 * m, max_ctx - 1);
+            vw[m] = *reinterpret_cast<const u32x4 *>(vb + vp * rs + 8 * row);
+        }
+    }
+    const float2 *trow = reinterpret_cast<const float2 *>(cos_sin) + (size_t)(append ? pos : 0u) * half;
+    uint32_t qr[4][2];
+    float2 tq[4];
+#pragma unroll
+    for (uint32_t jj = 0; jj < 4; ++jj) {  // query pairs t, t + 256, ... of the G * 64
+        const uint32_t i0 = tid + 256 * jj, i = i0 < G * half ? i0 : 0u, g = i / half, d = i % half;
+        const uint16_t *src = q + ((size_t)b * q_heads + kvh * G + g) * D;
+        qr[jj][0] = src[d];
+        qr[jj][1] = src[d + half];
+        tq[jj] = trow[d];
+    }
+    uint32_t kn0, kn1, vn0, vn1;
+    {
+        const uint32_t tn = tid < half ? tid : 0u;
+        const uint16_t *ks = k + ((size_t)b * kv_heads + kvh) * D;
+        const uint16_t *vs = v + ((size_t)b * kv_heads + kvh) * D;
+        kn0 = ks[tn];
+        kn1 = ks[tn + half];
+        vn0 = vs[tn];
+        vn1 = vs[tn + half];
+    }
+    // 1. rotations into LDS
+#pragma unroll
+    for (uint32_t jj = 0; jj < 4; ++jj) {
+        const uint32_t i = tid + 256 * jj, g = i / half, d = i % half;
+        if (i < G * half) {
+            uint32_t b0 = qr[jj][0], b1 = qr[jj][1];
+            if (append) {
+                const float x0 = bf16_to_f32(b0), x1 = bf16_to_f32(b1);
+                const float2 t = tq[jj];
+                b0 = f32_to_bf16(fmaf(x0, t.x, -x1 * t.y));
+                b1 = f32_to_bf16(fmaf(x0, t.y, x1 * t.x));
+            }
+            qs[g * QS + d] = (uint16_t)b0;
+            qs[g * QS + d + half] = (uint16_t)b1;
+        }
+    }
+    if (has_new && tid < half) {  // tq[0] is the table row of d = tid
+        const float x0 = bf16_to_f32(kn0), x1 = bf16_to_f32(kn1);
+        kn0 = f32_to_bf16(fmaf(x0, tq[0].x, -x1 * tq[0].y));  // stored to the cache after the last
+        kn1 = f32_to_bf16(fmaf(x0, tq[0].y, x1 * tq[0].x));   // barrier (a barrier waits for stores)
+        knew[tid] = (uint16_t)kn0;
+        knew[tid + half] = (uint16_t)kn1;
+        vnew[tid] = (uint16_t)vn0;
+        vnew[tid + half] = (uint16_t)vn1;
+    }
+    __syncthreads();
+    // 2. scores of this wave's 16 positions
+    float sc[4];
+    {
+        const bool fresh = has_new && p0 + row == pos;  // column `row` is the new position
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (p0 < n) {  // uniform
+#pragma unroll
+            for (uint32_t s2 = 0; s2 < 4; ++s2) {
+                const u32x4 qa = row < G ? *reinterpret_cast<const u32x4 *>(&qs[row * QS + 32 * s2 + 8 * kq])
+                                         : u32x4{0, 0, 0, 0};
+                const u32x4 kb4 = fresh ? *reinterpret_cast<const u32x4 *>(&knew[32 * s2 + 8 * kq]) : kw[s2];
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, qa),
+                                                              __builtin_bit_cast(bf16x8_t, kb4), acc, 0, 0, 0);
+            }
+        }
+        const bool valid = p0 + row < n;
+        const float scale = 1.0f / sqrtf((float)D);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc[e] = valid ? acc[e] * scale : -INFINITY;
+    }
+    // 3. the wave's softmax statistics per head (lanes 16 kq .. hold heads 4 kq + e)
+    float mw[4], lw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        mw[e] = tree_max_from<2>(sc[e], (int)l);
+        sc[e] = sc[e] == -INFINITY ? 0.0f : expf(sc[e] - mw[e]);
+        lw[e] = tree_sum_from<2>(sc[e], (int)l);
+    }
+    // 4. values
+    f32x4 acc_o[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc_o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (p0 < n) {  // uniform
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pt[w][(4 * kq + e) * 16 + row] = sc[e];
+#pragma unroll
+        for (uint32_t m = 0; m < 4; ++m) {
+            const uint32_t pr = kq + 4 * m;  // tile row: position p0 + pr
+            u32x4 val = p0 + pr < n ? vw[m] : u32x4{0, 0, 0, 0};
+            if (has_new && p0 + pr == pos) val = *reinterpret_cast<const u32x4 *>(&vnew[8 * row]);
+            *reinterpret_cast<u32x4 *>(&vt[w][pr * VS + 8 * row]) = val;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        s16x4 ahi, alo;  // P[head row][positions 4 kq .. + 3]
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const float pv = pt[w][row * 16 + 4 * kq + i];
+            const uint32_t hi = f32_to_bf16(pv);
+            ahi[i] = (short)hi;
+            alo[i] = (short)f32_to_bf16(pv - bf16_to_f32(hi));
+        }
+#pragma unroll
+        for (uint32_t t = 0; t < 8; ++t) {
+            s16x4 bv;  // V[positions 4 kq .. + 3][dim 16 t + row]
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) bv[i] = (short)vt[w][(4 * kq + i) * VS + 16 * t + row];
+            acc_o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ahi, bv, acc_o[t], 0, 0, 0);
+            acc_o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(alo, bv, acc_o[t], 0, 0, 0);
+        }
+    }
+    // 5. the slice's partial: the waves merged in wave order
+    if (row == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            mrow[w][4 * kq + e] = mw[e];
+            lrow[w][4 * kq + e] = lw[e];
+        }
+    }
+#pragma unroll
+    for (uint32_t t = 0; t < 8; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) accm[w][(4 * kq + e) * AS + 16 * t + row] = acc_o[t][e];
+    __syncthreads();
+    for (uint32_t o = tid; o < G * D; o += 256) {
+        const uint32_t h = o / D, d = o % D;
+        float mv[4], lv[4], av[4];
+#pragma unroll
+        for (uint32_t ww = 0; ww < 4; ++ww) {
+            mv[ww] = mrow[ww][h];
+            lv[ww] = lrow[ww][h];
+            av[ww] = accm[ww][h * AS + d];
+        }
+        const float M = fmaxf(fmaxf(mv[0], mv[1]), fmaxf(mv[2], mv[3]));
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (uint32_t ww = 0; ww < 4; ++ww) {  // a wave without positions (m = -inf) adds nothing
+            const bool live = mv[ww] != -INFINITY;
+            const float wt = live ? expf(mv[ww] - M) : 0.0f;
+            L = live ? fmaf(wt, lv[ww], L) : L;
+            A = live ? fmaf(wt, av[ww], A) : A;
+        }
+        out[2 * G + h * D + d] = A;
+        if (d == 0) {
+            out[h] = M;
+            out[G + h] = L;
+        }
+    }
+    if (has_new && tid < half) {
+        const size_t cbase = (((size_t)b * max_ctx + pos) * kv_heads + kvh) * D;
+        k_cache[cbase + tid] = (uint16_t)kn0;
+        k_cache[cbase + tid + half] = (uint16_t)kn1;
+        v_cache[cbase + tid] = (uint16_t)vn0;
+        v_cache[cbase + tid + half] = (uint16_t)vn1;
+    }
+}
+
 // grid (q_heads, batch), 256 threads: merge the slices of one head in slice order.  Every slice
 // publishes (m, l) -- empty slices (-inf, 0) -- so the merge needs no slice count.  Slices are
 // taken in rounds of NI * 32 (NI = 256 / D interleaves): thread t reads (m, l) of slice t of the
@@ -737,13 +960,22 @@ hipError_t launch_rope_attention(const uint16_t *q, const uint16_t *k, const uin
                                  const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
                                  uint32_t D, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx, uint16_t *out,
                                  float *part, hipStream_t s) {
-    const uint32_t splits = attention_splits(max_ctx);
     const uint32_t G = q_heads / kv_heads;
+    // 64-position slices (head_dim 128): when they still give about one block per compute unit
+    // (16-position slices spread a short batch over more of them)
+    const uint32_t s64 = (max_ctx + kSplit64 - 1) / kSplit64;
+    const bool wide = D == 128 && G <= 16 &&
+                      (tuning().attn_slice64 == 2 ||
+                       (tuning().attn_slice64 == 1 && (uint64_t)batch * kv_heads * s64 >= (uint64_t)device_cus()));
+    const uint32_t splits = wide ? s64 : attention_splits(max_ctx);
     const dim3 grid(splits, kv_heads, batch);
 #define KR_SPLIT(GP)                                                                                           \
     hipLaunchKernelGGL(attention_split_kernel<GP>, grid, dim3(256), 0, s, q, k, v, cos_sin, positions, q_heads, \
                        kv_heads, D, k_cache, v_cache, max_ctx, part)
-    if (G <= 1)
+    if (wide)
+        hipLaunchKernelGGL(attention_split64_kernel, grid, dim3(256), 0, s, q, k, v, cos_sin, positions, q_heads,
+                           kv_heads, k_cache, v_cache, max_ctx, part);
+    else if (G <= 1)
         KR_SPLIT(1);
     else if (G <= 2)
         KR_SPLIT(2);

@@ -336,6 +336,10 @@ int kr_set_option(int option, int value) {
             if (value != 0 && value != 1) return fail(KR_E_INVALID, "prefill xcd split must be 0 or 1");
             tuning().prefill_xcd_split = value;
             return ok();
+        case KR_OPT_ATTN_SLICE64:
+            if (value < 0 || value > 2) return fail(KR_E_INVALID, "attention slice64 must be 0, 1 or 2");
+            tuning().attn_slice64 = value;
+            return ok();
         default: return fail(KR_E_INVALID, "unknown option %d", option);
     }
 }
@@ -355,6 +359,7 @@ int kr_get_option(int option) {
         case KR_OPT_MOE_COMBINE: return tuning().moe_combine;
         case KR_OPT_MOE_ROUTE_FUSED: return tuning().moe_route_fused;
         case KR_OPT_PREFILL_XCD_SPLIT: return tuning().prefill_xcd_split;
+        case KR_OPT_ATTN_SLICE64: return tuning().attn_slice64;
         case KR_OPT_GEMV_LONG_GROUPS: return tuning().gemv_long_groups;
         case KR_OPT_SPLITK_TICKETS: return tuning().splitk_tickets;
         case KR_OPT_ATTN_MERGE_WAVE: return tuning().attn_merge_wave;

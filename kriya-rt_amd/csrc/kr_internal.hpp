@@ -46,6 +46,8 @@ struct Tuning {
     int splitk_tickets = 1;            // few-token split K: 1 the last block of a run reduces, 0 a second launch
     int prefill_xcd_split = 1;         // prefill split K: each K split on its own XCDs (1) or the tile
                                        // grouping of unsplit launches (0)
+    int attn_slice64 = 1;              // decode attention, head_dim 128: slices of 64 positions when they give
+                                       // >= 1 block per CU (1), always (2), never: 16 (0)
     int attn_merge_wave = 1;           // decode attention merge of <= 64 slices, D a power of two 8..256:
                                        // 1 the barrier-free wave kernel, 0 the general block kernel
     int prefill_operands = 1;          // kr_q4_mlp at m >= 64: 1 fp16 operands converted once per call

@@ -41,6 +41,7 @@ OPT_SKINNY_DEPTH = 16
 OPT_MOE_COMBINE = 17
 OPT_MOE_ROUTE_FUSED = 18
 OPT_PREFILL_XCD_SPLIT = 19
+OPT_ATTN_SLICE64 = 20
 
 _lib = None
 

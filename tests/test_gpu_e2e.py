@@ -269,3 +269,44 @@ def test_decode_step_small_model(kq, batch):
         top2 = np.sort(want[b])[-2:]
         if top2[1] - top2[0] > 2 * bound:
             assert got_tok[b] == int(np.argmax(want[b]))
+
+
+@pytest.mark.parametrize("B,H,KVH,ctx,pos", [(2, 16, 2, 513, [512, 130]), (1, 16, 2, 1100, [1099]),
+                                             (2, 32, 2, 70, [64, 70]), (1, 8, 8, 16, [0]),
+                                             (3, 16, 2, 600, [599, 0, 300]), (2, 2, 2, 40, [39, 45]),
+                                             (1, 24, 2, 530, [529]), (1, 16, 2, 4200, [4100])])
+def test_attention_64_position_slices(kq, B, H, KVH, ctx, pos):
+    """head_dim 128 splits the context into slices of 64 positions (KR_OPT_ATTN_SLICE64 = 2 forces them; the
+    default takes them when they give a block per compute unit; one wave per 16 positions over all dims, the
+    block's waves merged into the slice's partial).  Against
+    kr_rope_kv_append + kr_attention_decode and against 16-position slices: the same caches, outputs within
+    a few bf16 ulps (the f32 sums run in another order).  pos >= ctx: no append, unrotated queries, the whole
+    cache; pos 0: only the new position; ctx 4200: 66 slices, the general merge kernel."""
+    from kriya_q4 import synth
+    from kriya_q4.qwen_decode import rope_table
+    D = 128
+    case(f"attention 64-position slices B={B} H={H}/{KVH} ctx={ctx} pos={pos}")
+    q = dev_bf16(synth.bf16_normal((B, H * D), 3520))
+    k = dev_bf16(synth.bf16_normal((B, KVH * D), 3521))
+    v = dev_bf16(synth.bf16_normal((B, KVH * D), 3522))
+    kc0 = dev_bf16(synth.bf16_normal((B, ctx, KVH, D), 3523))
+    vc0 = dev_bf16(synth.bf16_normal((B, ctx, KVH, D), 3524))
+    cs = rope_table(ctx, D, 1e6).cuda()
+    posd = torch.tensor(pos, dtype=torch.int32).cuda()
+    q1, kc1, vc1 = q.clone(), kc0.clone(), vc0.clone()
+    kq.rope_kv_append(q1, k, v, cs, posd, H, KVH, D, kc1, vc1)
+    want = kq.attention_decode(q1, kc1, vc1, posd, H, KVH, D).float().cpu().numpy()
+    outs = {}
+    try:
+        for wide in (2, 0):
+            kq.set_option(kq.OPT_ATTN_SLICE64, wide)
+            kc, vc = kc0.clone(), vc0.clone()
+            outs[wide] = kq.rope_attention_decode(q, k, v, cs, posd, H, KVH, D, kc, vc).float().cpu().numpy()
+            assert torch.equal(kc1.view(torch.int16), kc.view(torch.int16)), f"k cache, slice64={wide}"
+            assert torch.equal(vc1.view(torch.int16), vc.view(torch.int16)), f"v cache, slice64={wide}"
+    finally:
+        kq.set_option(kq.OPT_ATTN_SLICE64, 1)
+    for wide, g in outs.items():
+        assert np.all(np.isfinite(g)), wide
+        assert np.all(np.abs(g - want) <= np.abs(want) * 2.0 ** -7 + 1e-3 * np.abs(want).max()), f"slice64={wide}"
+    assert np.all(np.abs(outs[2] - outs[0]) <= np.abs(outs[0]) * 2.0 ** -7 + 1e-3 * np.abs(outs[0]).max())
