@@ -83,6 +83,27 @@ int kr_rope_attention_decode(const uint16_t *q, const uint16_t *k, const uint16_
                              uint32_t head_dim, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx,
                              uint16_t *out, void *workspace, size_t workspace_bytes, void *stream);
 
+/* The attention block's tail: RoPE + KV append + decode attention, then the
+ * output projection accumulated into the residual,
+ *   h[b] (+)= attention(q, k, v, ...)[b] . o_proj^T,
+ * i.e. kr_rope_attention_decode followed by kr_q4_linear(o_proj, attn, h,
+ * accumulate = 1) (the o_proj step of the reference's decode layer,
+ * encoder.rs:4880-5484).  With one sequence, head_dim 128, q_heads <= 16 and at
+ * most 16 slices of 64 positions (max_ctx <= 1024), the slices' merge runs
+ * inside the projection's launch (every block merges the partials into x
+ * itself): two launches instead of three (KR_OPT_ATTN_MERGE_OPROJ).  Results
+ * within f32 summation order of the two calls.  o_proj: Q4 [n, q_heads *
+ * head_dim]; h: [batch, n] bf16 or f32 (h_dtype), updated in place.
+ * workspace: kr_attention_q4_out_workspace_bytes(batch, q_heads, head_dim,
+ * max_ctx) bytes, 16-byte aligned; calls sharing it must not overlap in time.
+ * Limits: those of kr_rope_attention_decode and kr_q4_linear. */
+size_t kr_attention_q4_out_workspace_bytes(uint32_t batch, uint32_t q_heads, uint32_t head_dim, uint32_t max_ctx);
+int kr_rope_attention_q4_out(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *cos_sin,
+                             const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                             uint32_t head_dim, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx,
+                             const kr_q4_matrix *o_proj, void *h, int h_dtype, void *workspace, size_t workspace_bytes,
+                             void *stream);
+
 /* Greedy sampling (transformer_glue.metal:407-494, temperature 0):
  * out[r] = index of the largest logits[r, :] (ties to the lowest index, NaN never taken). */
 int kr_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, void *stream);

@@ -136,6 +136,9 @@ const char *kr_last_error(void);
                                          * over the dims): 1 (default) when batch * kv_heads * slices still
                                          * gives one block per compute unit, 2 always, 0 never.  The f32
                                          * sums differ in order. */
+#define KR_OPT_ATTN_MERGE_OPROJ 21      /* kr_rope_attention_q4_out with one sequence, head_dim 128: 1 (default)
+                                         * the slices' merge runs inside the output projection's launch;
+                                         * 0 kr_rope_attention_decode, then kr_q4_linear (accumulate). */
 int kr_set_option(int option, int value);
 int kr_get_option(int option);
 

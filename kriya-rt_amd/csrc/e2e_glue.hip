@@ -13,6 +13,7 @@
 #include <math.h>
 
 #include "kr_internal.hpp"
+#include "q4_dot2.hpp"
 
 namespace kr {
 
@@ -524,7 +525,8 @@ __global__ __launch_bounds__(256) void attention_split_kernel(const uint16_t *q,
 // partials the merge reads.
 constexpr uint32_t kSplit64 = 64;
 
-__global__ __launch_bounds__(256) void attention_split64_kernel(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+template <uint32_t NW>  // waves per block: slices of 16 NW positions (4: the 64 of the name)
+__global__ __launch_bounds__(64 * NW) void attention_split64_kernel(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                                                                 const float *cos_sin, const uint32_t *positions,
                                                                 uint32_t q_heads, uint32_t kv_heads, uint16_t *k_cache,
                                                                 uint16_t *v_cache, uint32_t max_ctx, float *part) {
@@ -535,10 +537,11 @@ __global__ __launch_bounds__(256) void attention_split64_kernel(const uint16_t *
     typedef short s16x4 __attribute__((ext_vector_type(4)));
     __shared__ __align__(16) uint16_t qs[16 * QS];           // rotated queries, bf16 [head][dim]
     __shared__ __align__(16) uint16_t knew[D], vnew[D];      // the new key (rotated) and value
-    __shared__ __align__(16) uint16_t vt[4][16 * VS];        // per-wave value tile [position][dim]
-    __shared__ __align__(16) float pt[4][16 * 16];           // per-wave probability tile [head][position]
-    __shared__ float mrow[4][16], lrow[4][16];
-    __shared__ __align__(16) float accm[4][16 * AS];         // per-wave unnormalised outputs [head][dim]
+    constexpr uint32_t kLen = 16 * NW, kThreads = 64 * NW;
+    __shared__ __align__(16) uint16_t vt[NW][16 * VS];       // per-wave value tile [position][dim]
+    __shared__ __align__(16) float pt[NW][16 * 16];          // per-wave probability tile [head][position]
+    __shared__ float mrow[NW][16], lrow[NW][16];
+    __shared__ __align__(16) float accm[NW][16 * AS];        // per-wave unnormalised outputs [head][dim]
     const uint32_t tid = threadIdx.x, l = tid & 63, row = l & 15, kq = l >> 4;
     const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, splits = gridDim.x;
@@ -546,7 +549,7 @@ __global__ __launch_bounds__(256) void attention_split64_kernel(const uint16_t *
     const uint32_t pos = __builtin_amdgcn_readfirstlane(positions[b]);
     const bool append = pos < max_ctx;
     const uint32_t n = min(pos, max_ctx - 1) + 1;  // positions attended
-    const uint32_t s0 = s * kSplit64, p0 = s0 + 16 * w;
+    const uint32_t s0 = s * kLen, p0 = s0 + 16 * w;
     float *out = part + (((size_t)b * kv_heads + kvh) * splits + s) * (size_t)G * (D + 2);  // m[G], l[G], acc[G][D]
     if (s0 >= n) {  // nothing of this sequence in the slice
         if (tid < G) {
@@ -555,7 +558,7 @@ __global__ __launch_bounds__(256) void attention_split64_kernel(const uint16_t *
         }
         return;
     }
-    const bool has_new = append && pos >= s0 && pos < s0 + kSplit64;
+    const bool has_new = append && pos >= s0 && pos < s0 + kLen;
     const size_t rs = (size_t)kv_heads * D;
     const uint16_t *kb = k_cache + ((size_t)b * max_ctx * kv_heads + kvh) * D;
     const uint16_t *vb = v_cache + ((size_t)b * max_ctx * kv_heads + kvh) * D;
@@ -572,11 +575,12 @@ __global__ __launch_bounds__(256) void attention_split64_kernel(const uint16_t *
         }
     }
     const float2 *trow = reinterpret_cast<const float2 *>(cos_sin) + (size_t)(append ? pos : 0u) * half;
-    uint32_t qr[4][2];
-    float2 tq[4];
+    constexpr uint32_t kQP = 1024 / kThreads;  // query pairs per thread (G * 64 <= 1024)
+    uint32_t qr[kQP][2];
+    float2 tq[kQP];
 #pragma unroll
-    for (uint32_t jj = 0; jj < 4; ++jj) {  // query pairs t, t + 256, ... of the G * 64
-        const uint32_t i0 = tid + 256 * jj, i = i0 < G * half ? i0 : 0u, g = i / half, d = i % half;
+    for (uint32_t jj = 0; jj < kQP; ++jj) {  // query pairs t, t + kThreads, ... of the G * 64
+        const uint32_t i0 = tid + kThreads * jj, i = i0 < G * half ? i0 : 0u, g = i / half, d = i % half;
         const uint16_t *src = q + ((size_t)b * q_heads + kvh * G + g) * D;
         qr[jj][0] = src[d];
         qr[jj][1] = src[d + half];
@@ -594,8 +598,8 @@ __global__ __launch_bounds__(256) void attention_split64_kernel(const uint16_t *
     }
     // 1. rotations into LDS
 #pragma unroll
-    for (uint32_t jj = 0; jj < 4; ++jj) {
-        const uint32_t i = tid + 256 * jj, g = i / half, d = i % half;
+    for (uint32_t jj = 0; jj < kQP; ++jj) {
+        const uint32_t i = tid + kThreads * jj, g = i / half, d = i % half;
         if (i < G * half) {
             uint32_t b0 = qr[jj][0], b1 = qr[jj][1];
             if (append) {
@@ -693,19 +697,21 @@ __global__ __launch_bounds__(256) void attention_split64_kernel(const uint16_t *
 #pragma unroll
         for (int e = 0; e < 4; ++e) accm[w][(4 * kq + e) * AS + 16 * t + row] = acc_o[t][e];
     __syncthreads();
-    for (uint32_t o = tid; o < G * D; o += 256) {
+    for (uint32_t o = tid; o < G * D; o += kThreads) {
         const uint32_t h = o / D, d = o % D;
-        float mv[4], lv[4], av[4];
+        float mv[NW], lv[NW], av[NW];
 #pragma unroll
-        for (uint32_t ww = 0; ww < 4; ++ww) {
+        for (uint32_t ww = 0; ww < NW; ++ww) {
             mv[ww] = mrow[ww][h];
             lv[ww] = lrow[ww][h];
             av[ww] = accm[ww][h * AS + d];
         }
-        const float M = fmaxf(fmaxf(mv[0], mv[1]), fmaxf(mv[2], mv[3]));
+        float M = mv[0];
+#pragma unroll
+        for (uint32_t ww = 1; ww < NW; ++ww) M = fmaxf(M, mv[ww]);
         float L = 0.0f, A = 0.0f;
 #pragma unroll
-        for (uint32_t ww = 0; ww < 4; ++ww) {  // a wave without positions (m = -inf) adds nothing
+        for (uint32_t ww = 0; ww < NW; ++ww) {  // a wave without positions (m = -inf) adds nothing
             const bool live = mv[ww] != -INFINITY;
             const float wt = live ? expf(mv[ww] - M) : 0.0f;
             L = live ? fmaf(wt, lv[ww], L) : L;
@@ -724,6 +730,157 @@ __global__ __launch_bounds__(256) void attention_split64_kernel(const uint16_t *
         v_cache[cbase + tid] = (uint16_t)vn0;
         v_cache[cbase + tid + half] = (uint16_t)vn1;
     }
+}
+
+// attention_merge_oproj_kernel: one sequence's attention slices merged and multiplied by the output
+// projection in one launch: h[row] (+)= x . W[row] with
+//   x[head, d] = bf16(sum_s w_hs acc_s[head, d] / L_h),  w_hs = e^(m_s - M_h),  M_h = max_s m_s,
+//   L_h = sum_s w_hs l_s   (slices in order; a slice of weight 0 is skipped, not multiplied),
+// over the partials (m, l, acc) the split kernels write.  Grid ceil(n / 8), 256 threads: every block
+// merges all of x into LDS (each output row needs all of it), then wave w computes rows 8 b + 2 w and
+// 8 b + 2 w + 1 with the m == 1 GEMV's arithmetic (one 16-byte chunk per lane, chunk_dot, the fixed
+// reduction tree).  The weights, the partials and the old outputs are all requested first.  head_dim
+// 128; n = rows of W, k = q_heads * 128 <= 2048; splits <= kMergeMaxSlices.
+constexpr uint32_t kMergeMaxSlices = kMergeOprojMaxSlices;
+
+template <uint32_t NS>  // slices held in registers (>= splits)
+__global__ __launch_bounds__(256) void attention_merge_oproj_kernel(const float *part, uint32_t q_heads,
+                                                                    uint32_t kv_heads, uint32_t splits, Q4Mat W,
+                                                                    void *h, int h_f32) {
+    constexpr uint32_t D = 128;
+    __shared__ float s_m[16][kMergeMaxSlices], s_l[16][kMergeMaxSlices];
+    __shared__ float s_w[16][kMergeMaxSlices], s_L[16];
+    __shared__ u32x4 s_x[256];  // x, bf16, 8 values per unit
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t G = q_heads / kv_heads, K = W.k, nchunks = K >> 5, wpr = K >> 3, groups = K >> 6;
+    const size_t slice = (size_t)G * (D + 2);  // floats of one (kv head, slice) partial
+    // 1. requests: the wave's two weight rows (chunk `lane`), the old outputs, the partials
+    const bool live = lane < nchunks;
+    const uint32_t c = live ? lane : 0u;
+    const uint32_t r0 = blockIdx.x * 8 + 2 * wave;
+    u32x4 wv[2];
+    uint32_t sv[2], bv[2];
+#pragma unroll
+    for (uint32_t r = 0; r < 2; ++r) {
+        const size_t row = min(r0 + r, W.n - 1);  // a tail row is never stored
+        wv[r] = ld_stream(reinterpret_cast<const u32x4 *>(W.qw + row * wpr) + c);
+        sv[r] = ld_stream(W.sc + row * groups + (c >> 1));
+        bv[r] = ld_stream(W.bi + row * groups + (c >> 1));
+    }
+    float pre = 0.0f;  // lanes 0 and 32 store rows r0, r0 + 1
+    if ((lane & 31) == 0 && r0 + (lane >> 5) < W.n) {
+        const uint32_t row = r0 + (lane >> 5);
+        pre = h_f32 ? reinterpret_cast<const float *>(h)[row] : bf16_to_f32(reinterpret_cast<const uint16_t *>(h)[row]);
+    }
+    // (m, l) of (head, slice) for thread t < q_heads * splits
+    float mt = -INFINITY, lt = 0.0f;
+    {
+        const uint32_t t = tid < q_heads * splits ? tid : 0u, hh = t / splits, sl = t % splits;
+        const float *pb = part + ((size_t)(hh / G) * splits + sl) * slice;
+        mt = pb[hh % G];
+        lt = pb[G + hh % G];
+    }
+    // the acc units of thread t < K / 8: head t / 16, dims 8 (t % 16) .. + 7, every slice
+    const uint32_t units = K >> 3;
+    const uint32_t ut = tid < units ? tid : 0u, uh = ut >> 4, ud = 8 * (ut & 15);
+    f32x4 av[NS][2];
+    {
+        const float *pb = part + (size_t)(uh / G) * splits * slice + 2 * G + (uh % G) * D + ud;
+#pragma unroll
+        for (uint32_t sl = 0; sl < NS; ++sl) {
+            const float *ps = pb + (size_t)min(sl, splits - 1) * slice;
+            av[sl][0] = *reinterpret_cast<const f32x4 *>(ps);
+            av[sl][1] = *reinterpret_cast<const f32x4 *>(ps + 4);
+        }
+    }
+    // 2. per head: M, the slice weights and L (one thread per head, slices in order)
+    if (tid < q_heads * splits) {
+        s_m[tid / splits][tid % splits] = mt;
+        s_l[tid / splits][tid % splits] = lt;
+    }
+    __syncthreads();
+    if (tid < q_heads) {
+        float M = -INFINITY;
+        for (uint32_t sl = 0; sl < splits; ++sl) M = fmaxf(M, s_m[tid][sl]);
+        float L = 0.0f;
+        for (uint32_t sl = 0; sl < splits; ++sl) {
+            const float m = s_m[tid][sl];
+            const float w = m == -INFINITY ? 0.0f : expf(m - M);
+            s_w[tid][sl] = w;
+            L = fmaf(w, s_l[tid][sl], L);
+        }
+        s_L[tid] = L;
+    }
+    __syncthreads();
+    // 3. x units into LDS
+    if (tid < units) {
+        f32x4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t sl = 0; sl < NS; ++sl) {
+            const float w = sl < splits ? s_w[uh][sl] : 0.0f;
+            if (w != 0.0f) {  // an empty slice's acc is never read
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    a0[e] = fmaf(w, av[sl][0][e], a0[e]);
+                    a1[e] = fmaf(w, av[sl][1][e], a1[e]);
+                }
+            }
+        }
+        const float L = s_L[uh];
+        s_x[tid] = u32x4{pack_bf16_rne(a0[0] / L, a0[1] / L), pack_bf16_rne(a0[2] / L, a0[3] / L),
+                         pack_bf16_rne(a1[0] / L, a1[1] / L), pack_bf16_rne(a1[2] / L, a1[3] / L)};
+    }
+    __syncthreads();
+    // 4. the wave's two rows
+    uint32_t X[16];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+        const u32x4 u = s_x[4 * c + qd];
+        X[4 * qd] = u.x;
+        X[4 * qd + 1] = u.y;
+        X[4 * qd + 2] = u.z;
+        X[4 * qd + 3] = u.w;
+    }
+    XChunk xc;
+    build_xchunk(xc, X, sgpr_const(0x05040100u), sgpr_const(0x07060302u));
+    const uint32_t kMask = sgpr_const(0x000F000Fu);
+    const uint32_t kMagic = vgpr_const(0x43004300u);
+    float acc[2];
+#pragma unroll
+    for (uint32_t r = 0; r < 2; ++r) {
+        const float d = chunk_dot(wv[r], sv[r], bv[r], xc, 0.0f, kMask, kMagic);
+        acc[r] = live ? d : 0.0f;
+    }
+    const float tot = wave_reduce_rows<2>(acc, (int)lane);  // lanes 0..31 row r0, 32..63 row r0 + 1
+    if ((lane & 31) == 0 && r0 + (lane >> 5) < W.n) {
+        const uint32_t row = r0 + (lane >> 5);
+        if (h_f32) reinterpret_cast<float *>(h)[row] = pre + tot;
+        else reinterpret_cast<uint16_t *>(h)[row] = (uint16_t)f32_to_bf16(tot + pre);
+    }
+}
+
+hipError_t launch_attention_merge_oproj(const float *part, uint32_t q_heads, uint32_t kv_heads, uint32_t splits,
+                                        const Q4Mat &w, void *h, int h_f32, hipStream_t s) {
+    if (splits == 0 || splits > kMergeMaxSlices || w.k != q_heads * 128 || w.k > 2048 || q_heads > 16)
+        return hipErrorInvalidValue;
+    const dim3 grid((w.n + 7) / 8);
+    if (splits <= 4) hipLaunchKernelGGL(attention_merge_oproj_kernel<4>, grid, dim3(256), 0, s, part, q_heads, kv_heads, splits, w, h, h_f32);
+    else if (splits <= 8) hipLaunchKernelGGL(attention_merge_oproj_kernel<8>, grid, dim3(256), 0, s, part, q_heads, kv_heads, splits, w, h, h_f32);
+    else if (splits <= 12) hipLaunchKernelGGL(attention_merge_oproj_kernel<12>, grid, dim3(256), 0, s, part, q_heads, kv_heads, splits, w, h, h_f32);
+    else hipLaunchKernelGGL(attention_merge_oproj_kernel<16>, grid, dim3(256), 0, s, part, q_heads, kv_heads, splits, w, h, h_f32);
+    return hipGetLastError();
+}
+
+uint32_t attention_slices64(uint32_t max_ctx) { return (max_ctx + kSplit64 - 1) / kSplit64; }
+
+hipError_t launch_rope_attention_partials64(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                            const float *cos_sin, const uint32_t *positions, uint32_t batch,
+                                            uint32_t q_heads, uint32_t kv_heads, uint16_t *k_cache,
+                                            uint16_t *v_cache, uint32_t max_ctx, float *part, hipStream_t s) {
+    hipLaunchKernelGGL(attention_split64_kernel<4>, dim3(attention_slices64(max_ctx), kv_heads, batch), dim3(256), 0, s,
+                       q, k, v, cos_sin, positions, q_heads, kv_heads, k_cache, v_cache, max_ctx, part);
+    return hipGetLastError();
 }
 
 // grid (q_heads, batch), 256 threads: merge the slices of one head in slice order.  Every slice
@@ -973,7 +1130,7 @@ hipError_t launch_rope_attention(const uint16_t *q, const uint16_t *k, const uin
     hipLaunchKernelGGL(attention_split_kernel<GP>, grid, dim3(256), 0, s, q, k, v, cos_sin, positions, q_heads, \
                        kv_heads, D, k_cache, v_cache, max_ctx, part)
     if (wide)
-        hipLaunchKernelGGL(attention_split64_kernel, grid, dim3(256), 0, s, q, k, v, cos_sin, positions, q_heads,
+        hipLaunchKernelGGL(attention_split64_kernel<4>, grid, dim3(256), 0, s, q, k, v, cos_sin, positions, q_heads,
                            kv_heads, k_cache, v_cache, max_ctx, part);
     else if (G <= 1)
         KR_SPLIT(1);

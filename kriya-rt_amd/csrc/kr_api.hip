@@ -336,6 +336,10 @@ int kr_set_option(int option, int value) {
             if (value != 0 && value != 1) return fail(KR_E_INVALID, "prefill xcd split must be 0 or 1");
             tuning().prefill_xcd_split = value;
             return ok();
+        case KR_OPT_ATTN_MERGE_OPROJ:
+            if (value != 0 && value != 1) return fail(KR_E_INVALID, "attention merge o_proj must be 0 or 1");
+            tuning().attn_merge_oproj = value;
+            return ok();
         case KR_OPT_ATTN_SLICE64:
             if (value < 0 || value > 2) return fail(KR_E_INVALID, "attention slice64 must be 0, 1 or 2");
             tuning().attn_slice64 = value;
@@ -360,6 +364,7 @@ int kr_get_option(int option) {
         case KR_OPT_MOE_ROUTE_FUSED: return tuning().moe_route_fused;
         case KR_OPT_PREFILL_XCD_SPLIT: return tuning().prefill_xcd_split;
         case KR_OPT_ATTN_SLICE64: return tuning().attn_slice64;
+        case KR_OPT_ATTN_MERGE_OPROJ: return tuning().attn_merge_oproj;
         case KR_OPT_GEMV_LONG_GROUPS: return tuning().gemv_long_groups;
         case KR_OPT_SPLITK_TICKETS: return tuning().splitk_tickets;
         case KR_OPT_ATTN_MERGE_WAVE: return tuning().attn_merge_wave;
@@ -1132,6 +1137,54 @@ int kr_rope_attention_decode(const uint16_t *q, const uint16_t *k, const uint16_
     return hip_status(launch_rope_attention(q, k, v, cos_sin, positions, batch, q_heads, kv_heads, head_dim, k_cache,
                                             v_cache, max_ctx, out, (float *)workspace, (hipStream_t)stream),
                       "kr_rope_attention_decode");
+}
+
+size_t kr_attention_q4_out_workspace_bytes(uint32_t batch, uint32_t q_heads, uint32_t head_dim, uint32_t max_ctx) {
+    // the slices' partials, then the attention output [batch, q_heads * head_dim] bf16 (unfused path)
+    return round_up(attention_workspace_bytes(batch, q_heads, head_dim, max_ctx), 256) +
+           round_up((size_t)batch * q_heads * head_dim * 2, 256);
+}
+
+int kr_rope_attention_q4_out(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *cos_sin,
+                             const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
+                             uint32_t head_dim, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx,
+                             const kr_q4_matrix *o_proj, void *h, int h_dtype, void *workspace, size_t workspace_bytes,
+                             void *stream) {
+    // every check of both stages first: a failing call enqueues nothing
+    if (int rc = check_heads(q_heads, kv_heads, head_dim, max_ctx)) return rc;
+    if (q_heads / kv_heads > kGlueMaxGroup)
+        return fail(KR_E_SHAPE, "q_heads / kv_heads = %u exceeds %u", q_heads / kv_heads, kGlueMaxGroup);
+    if (int rc = check_matrix(o_proj, "o_proj")) return rc;
+    if (o_proj->k != q_heads * head_dim)
+        return fail(KR_E_SHAPE, "o_proj k=%u must be q_heads * head_dim = %u", o_proj->k, q_heads * head_dim);
+    if (!valid_dtype(h_dtype)) return fail(KR_E_INVALID, "h_dtype %d invalid", h_dtype);
+    if (batch == 0) return ok();
+    if (!q || !k || !v || !cos_sin || !positions || !k_cache || !v_cache || !h) return fail(KR_E_INVALID, "NULL pointer");
+    if (!aligned(k_cache, 16) || !aligned(v_cache, 16)) return fail(KR_E_ALIGN, "k_cache and v_cache must be 16-byte aligned");
+    if (!aligned(cos_sin, 8)) return fail(KR_E_ALIGN, "cos_sin must be 8-byte aligned");
+    if (!aligned(h, dtype_size(h_dtype))) return fail(KR_E_ALIGN, "h misaligned");
+    if (batch > 65535) return fail(KR_E_SHAPE, "batch=%u exceeds 65535", batch);
+    const size_t need = kr_attention_q4_out_workspace_bytes(batch, q_heads, head_dim, max_ctx);
+    if (!workspace || workspace_bytes < need)
+        return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    if (!aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    float *part = (float *)workspace;
+    const uint32_t slices = attention_slices64(max_ctx);
+    if (tuning().attn_merge_oproj && batch == 1 && head_dim == 128 && q_heads <= 16 && o_proj->k <= 2048 &&
+        slices <= kMergeOprojMaxSlices && (uint64_t)slices * q_heads * (head_dim + 2) * 4 <= need) {
+        if (hipError_t e = launch_rope_attention_partials64(q, k, v, cos_sin, positions, batch, q_heads, kv_heads,
+                                                            k_cache, v_cache, max_ctx, part, s))
+            return hip_status(e, "kr_rope_attention_q4_out (attention)");
+        return hip_status(launch_attention_merge_oproj(part, q_heads, kv_heads, slices, to_mat(o_proj), h,
+                                                       h_dtype == KR_DTYPE_F32, s),
+                          "kr_rope_attention_q4_out (merge + o_proj)");
+    }
+    uint16_t *attn = (uint16_t *)((char *)workspace + round_up(attention_workspace_bytes(batch, q_heads, head_dim, max_ctx), 256));
+    if (int rc = kr_rope_attention_decode(q, k, v, cos_sin, positions, batch, q_heads, kv_heads, head_dim, k_cache,
+                                          v_cache, max_ctx, attn, workspace, need, stream))
+        return rc;
+    return kr_q4_linear(o_proj, attn, batch, h, h_dtype, 1, stream);
 }
 
 int kr_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, void *stream) {

@@ -48,6 +48,8 @@ struct Tuning {
                                        // grouping of unsplit launches (0)
     int attn_slice64 = 1;              // decode attention, head_dim 128: slices of 64 positions when they give
                                        // >= 1 block per CU (1), always (2), never: 16 (0)
+    int attn_merge_oproj = 1;          // kr_rope_attention_q4_out, one sequence: the merge inside the output
+                                       // projection's launch (1) or kr_rope_attention_decode + kr_q4_linear (0)
     int attn_merge_wave = 1;           // decode attention merge of <= 64 slices, D a power of two 8..256:
                                        // 1 the barrier-free wave kernel, 0 the general block kernel
     int prefill_operands = 1;          // kr_q4_mlp at m >= 64: 1 fp16 operands converted once per call
@@ -243,6 +245,17 @@ hipError_t launch_attention_decode(const uint16_t *q, const uint16_t *k_cache, c
 hipError_t launch_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, hipStream_t s);
 constexpr uint32_t kGlueMaxGroup = 16;  // query heads per kv head of the split attention
 size_t attention_workspace_bytes(uint32_t batch, uint32_t q_heads, uint32_t D, uint32_t max_ctx);
+// One sequence: the 64-position-slice partials of kr_rope_attention_decode (head_dim 128, G <= 16)
+// and their merge fused into the output projection h (+)= x . W^T (w.k = q_heads * 128 <= 2048,
+// at most 16 slices).
+constexpr uint32_t kMergeOprojMaxSlices = 16;
+uint32_t attention_slices64(uint32_t max_ctx);
+hipError_t launch_rope_attention_partials64(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                                            const float *cos_sin, const uint32_t *positions, uint32_t batch,
+                                            uint32_t q_heads, uint32_t kv_heads, uint16_t *k_cache,
+                                            uint16_t *v_cache, uint32_t max_ctx, float *part, hipStream_t s);
+hipError_t launch_attention_merge_oproj(const float *part, uint32_t q_heads, uint32_t kv_heads, uint32_t splits,
+                                        const Q4Mat &w, void *h, int h_f32, hipStream_t s);
 hipError_t launch_rope_attention(const uint16_t *q, const uint16_t *k, const uint16_t *v, const float *cos_sin,
                                  const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
                                  uint32_t D, uint16_t *k_cache, uint16_t *v_cache, uint32_t max_ctx, uint16_t *out,

@@ -42,6 +42,7 @@ OPT_MOE_COMBINE = 17
 OPT_MOE_ROUTE_FUSED = 18
 OPT_PREFILL_XCD_SPLIT = 19
 OPT_ATTN_SLICE64 = 20
+OPT_ATTN_MERGE_OPROJ = 21
 
 _lib = None
 
@@ -108,6 +109,9 @@ def lib():
             "kr_rmsnorm_q4_mlp_workspace_bytes": (sz, [u32, u32, u32]),
             "kr_rmsnorm_q4_mlp": (i32, [M, M, M, vp, vp, ctypes.c_float, u32, i32, vp, sz, vp]),
             "kr_rope_attention_decode": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, u32, vp, vp, sz, vp]),
+            "kr_attention_q4_out_workspace_bytes": (sz, [u32, u32, u32, u32]),
+            "kr_rope_attention_q4_out": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, u32, M, vp, i32, vp, sz,
+                                               vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -484,6 +488,24 @@ def rope_attention_decode(q, k, v, cos_sin, positions, q_heads, kv_heads, head_d
                                           _ptr(workspace), workspace.numel() * workspace.element_size(),
                                           _stream(stream)))
     return out
+
+
+def attention_q4_out_workspace(batch, q_heads, head_dim, max_ctx, device="cuda") -> torch.Tensor:
+    n = int(lib().kr_attention_q4_out_workspace_bytes(batch, q_heads, head_dim, max_ctx))
+    return torch.empty(max(n, 16), dtype=torch.uint8, device=device)
+
+
+def rope_attention_q4_out(q, k, v, cos_sin, positions, q_heads, kv_heads, head_dim, k_cache, v_cache,
+                          o_proj: "Q4Matrix", h: torch.Tensor, workspace=None, stream=None) -> torch.Tensor:
+    """h += rope_attention_decode(...) . o_proj^T (kr_rope_attention_q4_out); h bf16 or f32 [batch, n]."""
+    batch = int(positions.numel())
+    max_ctx = int(k_cache.shape[1])
+    if workspace is None:
+        workspace = attention_q4_out_workspace(batch, q_heads, head_dim, max_ctx, device=q.device)
+    _check(lib().kr_rope_attention_q4_out(_ptr(q), _ptr(k), _ptr(v), _ptr(cos_sin), _ptr(positions), batch, q_heads,
+                                          kv_heads, head_dim, _ptr(k_cache), _ptr(v_cache), max_ctx, o_proj.desc,
+                                          _ptr(h), _dt_of(h), _ptr(workspace), workspace.numel(), _stream(stream)))
+    return h
 
 
 def argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:

@@ -8,9 +8,10 @@ crates/kriya-backend-metal/src/encoder.rs:4880-5484) for a dense Qwen2 layer:
     q, k, v = x Wq^T + bq, x Wk^T + bk, x Wv^T + bv  encode_fused_qkv (:2539-2619); one launch with
                                                      the norm fused in at batch 1
     rope(q, k) at the position; append k, v          paged_gqa_and_deltanet.metal:115-222
-    a = attention(q, K[0..pos], V[0..pos])           GQA decode (one split-context launch + a combine,
-                                                     rope and append fused in)
-    h += a Wo^T                                      encode_q4_linear_accumulate (:2497-2536)
+    a = attention(q, K[0..pos], V[0..pos])           GQA decode (one split-context launch, rope and
+                                                     append fused in)
+    h += a Wo^T                                      encode_q4_linear_accumulate (:2497-2536); at batch 1
+                                                     the slices' merge runs inside this launch
     x = rmsnorm(h, ln2)
     h += down(silu(gate x) * up x)                   encode_dense_mlp (:2851-2906); the norm fused into
                                                      the gate/up GEMV at batch 1
@@ -31,8 +32,8 @@ from typing import List
 
 import torch
 
-from . import (ACT_SWIGLU, DTYPE_BF16, DTYPE_F32, Q4Matrix, argmax, attention_workspace, embedding, lib, q4_linear,
-               rmsnorm, rmsnorm_mlp, rmsnorm_mlp_workspace, rmsnorm_qkv, rope_attention_decode)
+from . import (ACT_SWIGLU, DTYPE_BF16, DTYPE_F32, Q4Matrix, argmax, attention_q4_out_workspace, embedding, lib,
+               q4_linear, rmsnorm, rmsnorm_mlp, rmsnorm_mlp_workspace, rmsnorm_qkv, rope_attention_q4_out)
 
 
 @dataclasses.dataclass(frozen=True)
@@ -141,11 +142,10 @@ class QwenQ4Decoder:
         self.q = torch.empty((batch, c.q_heads * c.head_dim), dtype=torch.bfloat16, device=device)
         self.k = torch.empty((batch, kv), dtype=torch.bfloat16, device=device)
         self.v = torch.empty_like(self.k)
-        self.attn = torch.empty_like(self.q)
         self.logits = torch.empty((batch, c.vocab), dtype=torch.float32, device=device)
         self.next = torch.empty(batch, dtype=torch.int32, device=device)
         self.ws = rmsnorm_mlp_workspace(batch, c.hidden, c.inter, device=device)
-        self.attn_ws = attention_workspace(batch, c.q_heads, c.head_dim, self.max_ctx, device=device)
+        self.attn_ws = attention_q4_out_workspace(batch, c.q_heads, c.head_dim, self.max_ctx, device=device)
 
     def load_weights(self, archive) -> None:
         """Replaces the random weights with a checkpoint's (a kriya_q4.loader.Archive in the Hugging Face /
@@ -180,10 +180,8 @@ class QwenQ4Decoder:
         for L in self.layers:
             rmsnorm_qkv(self.h, L.ln1, c.eps, L.q, L.k, L.v, q_bias=L.bq, k_bias=L.bk, v_bias=L.bv,
                         out_dtype=DTYPE_BF16, outs=(self.q, self.k, self.v), xnorm=self.x, stream=stream)
-            rope_attention_decode(self.q, self.k, self.v, self.cos_sin, self.positions, c.q_heads, c.kv_heads,
-                                  c.head_dim, L.k_cache, L.v_cache, out=self.attn, workspace=self.attn_ws,
-                                  stream=stream)
-            q4_linear(L.o, self.attn, y=self.h, accumulate=True, stream=stream)
+            rope_attention_q4_out(self.q, self.k, self.v, self.cos_sin, self.positions, c.q_heads, c.kv_heads,
+                                  c.head_dim, L.k_cache, L.v_cache, L.o, self.h, workspace=self.attn_ws, stream=stream)
             rmsnorm_mlp(L.gate, L.up, L.down, self.h, L.ln2, c.eps, activation=ACT_SWIGLU, workspace=self.ws,
                         stream=stream)
         rmsnorm(self.h, self.ln_f, c.eps, out=self.x, stream=stream)

@@ -16,7 +16,7 @@ import torch
 
 import oracle as O
 from _decode_ref import attention_np, bf, decode_ref, rope_np
-from _util import assert_rms_close, dev_bf16, host_bits, q4_dev
+from _util import assert_rms_close, dev_bf16, host_bits, q4_dev, rms
 
 pytestmark = pytest.mark.gpu
 
@@ -310,3 +310,52 @@ def test_attention_64_position_slices(kq, B, H, KVH, ctx, pos):
         assert np.all(np.isfinite(g)), wide
         assert np.all(np.abs(g - want) <= np.abs(want) * 2.0 ** -7 + 1e-3 * np.abs(want).max()), f"slice64={wide}"
     assert np.all(np.abs(outs[2] - outs[0]) <= np.abs(outs[0]) * 2.0 ** -7 + 1e-3 * np.abs(outs[0]).max())
+
+
+@pytest.mark.parametrize("B,H,KVH,ctx,pos", [(1, 16, 2, 513, [512]), (1, 16, 2, 513, [130]), (1, 16, 2, 513, [0]),
+                                             (1, 16, 2, 513, [600]), (1, 8, 8, 1024, [1000]), (1, 4, 1, 64, [63]),
+                                             (2, 16, 2, 513, [512, 7]), (1, 16, 2, 1100, [1099])])
+@pytest.mark.parametrize("h_dtype", ["bf16", "f32"])
+def test_rope_attention_q4_out(kq, B, H, KVH, ctx, pos, h_dtype):
+    """kr_rope_attention_q4_out: h += attention . o_proj^T.  One sequence with at most 16 slices of 64 positions
+    merges the slices inside the projection's launch; within f32 summation order of kr_rope_attention_decode
+    followed by kr_q4_linear (accumulate), which it is with KR_OPT_ATTN_MERGE_OPROJ = 0 (the same caches
+    either way).  Also against the oracle's GEMV of the two-step attention.  Two sequences and ctx 1100
+    (18 slices) take the two calls."""
+    from kriya_q4 import synth
+    from kriya_q4.qwen_decode import rope_table
+    D, N = 128, 2048
+    case(f"rope attention + o_proj B={B} H={H}/{KVH} ctx={ctx} pos={pos} h {h_dtype}")
+    q = dev_bf16(synth.bf16_normal((B, H * D), 3620))
+    k = dev_bf16(synth.bf16_normal((B, KVH * D), 3621))
+    v = dev_bf16(synth.bf16_normal((B, KVH * D), 3622))
+    kc0 = dev_bf16(synth.bf16_normal((B, ctx, KVH, D), 3623))
+    vc0 = dev_bf16(synth.bf16_normal((B, ctx, KVH, D), 3624))
+    wq = synth.q4_weight(N, H * D, 3625)
+    wo = kq.Q4Matrix.from_numpy(*wq)
+    cs = rope_table(ctx, D, 1e6).cuda()
+    posd = torch.tensor(pos, dtype=torch.int32).cuda()
+    h0 = synth.bf16_normal((B, N), 3626)
+    outs, caches = {}, {}
+    try:
+        for fused in (1, 0):
+            kq.set_option(kq.OPT_ATTN_MERGE_OPROJ, fused)
+            kc, vc = kc0.clone(), vc0.clone()
+            h = dev_bf16(h0).clone() if h_dtype == "bf16" else torch.from_numpy(O.bf16_to_f32(h0)).cuda()
+            kq.rope_attention_q4_out(q, k, v, cs, posd, H, KVH, D, kc, vc, wo, h)
+            outs[fused] = h.float().cpu().numpy().astype(np.float64)
+            caches[fused] = (kc.view(torch.int16).cpu(), vc.view(torch.int16).cpu())
+    finally:
+        kq.set_option(kq.OPT_ATTN_MERGE_OPROJ, 1)
+    assert torch.equal(caches[0][0], caches[1][0]) and torch.equal(caches[0][1], caches[1][1])
+    # the oracle's projection of the two-step attention (kr_rope_kv_append + kr_attention_decode)
+    q1, kc1, vc1 = q.clone(), kc0.clone(), vc0.clone()
+    kq.rope_kv_append(q1, k, v, cs, posd, H, KVH, D, kc1, vc1)
+    att = host_bits(kq.attention_decode(q1, kc1, vc1, posd, H, KVH, D))
+    delta = O.q4_matmul(O.Q4Planar(*wq), att).astype(np.float64)
+    base = O.bf16_to_f32(h0).astype(np.float64)
+    r = rms(delta)
+    slack = (np.abs(base + delta) * 2.0 ** -8 if h_dtype == "bf16" else 0.0) + 2e-2 * r
+    for fused, got in outs.items():
+        assert np.all(np.abs(got - (base + delta)) <= slack), f"fused={fused}"
+    assert np.all(np.abs(outs[1] - outs[0]) <= slack)
