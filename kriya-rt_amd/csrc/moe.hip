@@ -135,10 +135,15 @@ __global__ __launch_bounds__(1024) void moe_topk_kernel(const float *logits, uin
     }
 }
 
+// Tokens up to which one block routes them all (a wave per token, in rounds) rather than a top-k
+// launch over 16-token blocks followed by the scan launch.  At 64 tokens (four rounds) one block
+// made the cfg4 T = 64 step 106 -> 118 us.
+constexpr uint32_t kRouteOneBlockTokens = 16;
+
 hipError_t launch_moe_route(const float *logits, uint32_t T, uint32_t E, uint32_t K, int normalize,
                             uint32_t *experts, float *weights, uint32_t *counts, uint32_t *offsets, uint32_t *sorted,
                             hipStream_t s) {
-    if (logits && T > 16) {
+    if (logits && T > kRouteOneBlockTokens) {
         // more tokens than one block routes in a round: top-k on ceil(T / 16) blocks, then the
         // counts, offsets and sorted list from the chosen experts (the same results)
         hipLaunchKernelGGL(moe_topk_kernel, dim3((T + 15) / 16), dim3(1024), 0, s, logits, T, E, K, normalize, experts,
