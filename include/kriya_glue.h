@@ -108,6 +108,15 @@ int kr_rope_attention_q4_out(const uint16_t *q, const uint16_t *k, const uint16_
  * out[r] = index of the largest logits[r, :] (ties to the lowest index, NaN never taken). */
 int kr_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, void *stream);
 
+/* The same greedy argmax (transformer_glue.metal:407-494, the same result bit for bit) with
+ * each row spread over several blocks and a second, one-wave merge launch: for long rows
+ * (a vocabulary of 151936 logits: one block per row reads at about 54 GB/s).  workspace:
+ * kr_argmax_workspace_bytes(rows, n) bytes, 8-byte aligned, no initial contents; calls
+ * sharing it must not overlap in time. */
+size_t kr_argmax_workspace_bytes(uint32_t rows, uint32_t n);
+int kr_argmax_ws(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, void *workspace,
+                 size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

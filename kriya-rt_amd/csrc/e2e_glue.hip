@@ -12,6 +12,8 @@
 //   gpu_token_sampler (greedy) kernels/metal/transformer_glue.metal:407-494
 #include <math.h>
 
+#include <algorithm>
+
 #include "kr_internal.hpp"
 #include "q4_dot2.hpp"
 
@@ -1078,6 +1080,94 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float *logits, uint3
     }
 }
 
+// Greedy argmax over a row spread across several blocks (rows with many logits: one block reads
+// a row at about 54 GB/s whatever its depth).  Block (j, r) takes logits [j per, (j + 1) per) of row
+// r and publishes (largest value, its first index) -- index kNoArg when it saw only NaN -- to
+// part[r][j]; argmax_merge_kernel then picks, per row, the largest value and among equal values the
+// lowest index.  Max-then-lowest-index is associative and commutative, so the result is the row's
+// first maximum (NaN never taken, a row of NaN gives 0) for any split: kr_argmax's result.
+constexpr uint32_t kNoArg = 0xFFFFFFFFu;
+
+struct ArgPart {
+    float v;
+    uint32_t i;
+};
+
+__device__ __forceinline__ void arg_take(float &v, uint32_t &idx, float ov, uint32_t oi) {
+    if (ov > v || (ov == v && oi < idx) || (idx == kNoArg && oi != kNoArg)) {
+        v = ov;
+        idx = oi;
+    }
+}
+
+// grid (P, rows), 256 threads; per % 4 == 0 when vec (rows of n % 4 == 0, 16-byte aligned)
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float *logits, uint32_t n, uint32_t per, int vec,
+                                                             ArgPart *part) {
+    __shared__ float bv[4];
+    __shared__ uint32_t bi[4];
+    const uint32_t tid = threadIdx.x, j = blockIdx.x, r = blockIdx.y;
+    const float *row = logits + (size_t)r * n;
+    const uint32_t e0 = j * per, e1 = min(e0 + per, n);
+    float v = -INFINITY;
+    uint32_t idx = kNoArg;
+    if (vec) {
+        // a cheap max per quad first (fmaxf drops NaN); a quad that can win is searched for its
+        // first lane holding that max; two quads requested before either is scanned
+        const f32x4 *r4 = reinterpret_cast<const f32x4 *>(row);
+        const uint32_t u0 = e0 / 4, u1 = (e1 + 3) / 4;
+        for (uint32_t i0 = u0 + tid; i0 < u1; i0 += 512) {
+            const uint32_t i1 = i0 + 256;
+            const f32x4 xa = r4[i0], xb = r4[min(i1, u1 - 1)];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t i = h ? i1 : i0;
+                const f32x4 x = h ? xb : xa;
+                const float m = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+                if (i < u1 && (m > v || (idx == kNoArg && m == m))) {
+                    const uint32_t c = x[0] == m ? 0u : x[1] == m ? 1u : x[2] == m ? 2u : 3u;
+                    v = m;
+                    idx = 4 * i + c;
+                }
+            }
+        }
+    } else {
+        for (uint32_t i = e0 + tid; i < e1; i += 256) {
+            const float x = row[i];
+            if (x > v || (idx == kNoArg && x == x)) {
+                v = x;
+                idx = i;
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) arg_take(v, idx, __shfl_xor(v, m), __shfl_xor(idx, m));
+    if ((tid & 63) == 0) {
+        bv[tid >> 6] = v;
+        bi[tid >> 6] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        v = bv[0];
+        idx = bi[0];
+        for (int w = 1; w < 4; ++w) arg_take(v, idx, bv[w], bi[w]);
+        part[(size_t)r * gridDim.x + j] = ArgPart{v, idx};
+    }
+}
+
+// grid rows, one wave: the row's P partials merged
+__global__ __launch_bounds__(64) void argmax_merge_kernel(const ArgPart *part, uint32_t P, uint32_t *out) {
+    const uint32_t lane = threadIdx.x, r = blockIdx.x;
+    float v = -INFINITY;
+    uint32_t idx = kNoArg;
+    for (uint32_t j = lane; j < P; j += 64) {
+        const ArgPart a = part[(size_t)r * P + j];
+        arg_take(v, idx, a.v, a.i);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) arg_take(v, idx, __shfl_xor(v, m), __shfl_xor(idx, m));
+    if (lane == 0) out[r] = idx == kNoArg ? 0u : idx;
+}
+
 hipError_t launch_q4_embedding(const Q4Mat &w, const uint32_t *tokens, uint32_t count, uint16_t *out, hipStream_t s) {
     const dim3 grid((w.k / 8 + 255) / 256, count);
     hipLaunchKernelGGL(q4_embedding_kernel, grid, dim3(256), 0, s, w, tokens, count, out);
@@ -1159,6 +1249,29 @@ hipError_t launch_rope_attention(const uint16_t *q, const uint16_t *k, const uin
     else
         hipLaunchKernelGGL(attention_combine_kernel, mgrid, dim3(256), 0, s, part, q_heads, kv_heads, D, splits, out);
 #undef KR_MERGE
+    return hipGetLastError();
+}
+
+// Blocks per row of the split argmax: about 512 blocks in all, at least 1024 logits each (so a
+// thread has a quad or more), at most kArgmaxMaxParts.
+uint32_t argmax_parts(uint32_t rows, uint32_t n) {
+    const uint32_t by_size = std::max<uint32_t>(1, n / 1024);
+    const uint32_t by_grid = std::max<uint32_t>(1, (512 + rows - 1) / std::max<uint32_t>(rows, 1));
+    return std::min<uint32_t>(std::min(by_size, by_grid), kArgmaxMaxParts);
+}
+
+size_t argmax_workspace_bytes(uint32_t rows, uint32_t n) { return (size_t)rows * argmax_parts(rows, n) * sizeof(ArgPart); }
+
+hipError_t launch_argmax_split(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, void *ws, hipStream_t s) {
+    const uint32_t P = argmax_parts(rows, n);
+    const int vec = n % 4 == 0 && (uintptr_t)logits % 16 == 0;
+    uint32_t per = (n + P - 1) / P;
+    if (vec) per = (per + 3) / 4 * 4;
+    ArgPart *part = reinterpret_cast<ArgPart *>(ws);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(P, rows), dim3(256), 0, s, logits, n, per, vec, part);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(argmax_merge_kernel, dim3(rows), dim3(64), 0, s, part, P, out);
     return hipGetLastError();
 }
 

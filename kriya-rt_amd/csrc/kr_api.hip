@@ -1195,6 +1195,23 @@ int kr_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, voi
     return hip_status(launch_argmax(logits, rows, n, out, (hipStream_t)stream), "kr_argmax");
 }
 
+size_t kr_argmax_workspace_bytes(uint32_t rows, uint32_t n) {
+    return rows == 0 || n == 0 ? 0 : round_up(argmax_workspace_bytes(rows, n), 256);
+}
+
+int kr_argmax_ws(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, void *workspace,
+                 size_t workspace_bytes, void *stream) {
+    if (rows == 0) return ok();
+    if (!logits || !out) return fail(KR_E_INVALID, "NULL pointer");
+    if (n == 0) return fail(KR_E_SHAPE, "n must be positive");
+    if (!aligned(logits, 4) || !aligned(out, 4)) return fail(KR_E_ALIGN, "logits/out misaligned");
+    const size_t need = kr_argmax_workspace_bytes(rows, n);
+    if (!workspace || workspace_bytes < need)
+        return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    if (!aligned(workspace, 8)) return fail(KR_E_ALIGN, "workspace must be 8-byte aligned");
+    return hip_status(launch_argmax_split(logits, rows, n, out, workspace, (hipStream_t)stream), "kr_argmax_ws");
+}
+
 
 }  // extern "C"
 

@@ -243,6 +243,11 @@ hipError_t launch_attention_decode(const uint16_t *q, const uint16_t *k_cache, c
                                    const uint32_t *positions, uint32_t batch, uint32_t q_heads, uint32_t kv_heads,
                                    uint32_t D, uint32_t max_ctx, uint16_t *out, hipStream_t s);
 hipError_t launch_argmax(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, hipStream_t s);
+// The same result from P blocks per row and a merge launch (workspace: argmax_workspace_bytes).
+constexpr uint32_t kArgmaxMaxParts = 512;
+uint32_t argmax_parts(uint32_t rows, uint32_t n);
+size_t argmax_workspace_bytes(uint32_t rows, uint32_t n);
+hipError_t launch_argmax_split(const float *logits, uint32_t rows, uint32_t n, uint32_t *out, void *ws, hipStream_t s);
 constexpr uint32_t kGlueMaxGroup = 16;  // query heads per kv head of the split attention
 size_t attention_workspace_bytes(uint32_t batch, uint32_t q_heads, uint32_t D, uint32_t max_ctx);
 // One sequence: the 64-position-slice partials of kr_rope_attention_decode (head_dim 128, G <= 16)

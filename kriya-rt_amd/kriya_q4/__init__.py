@@ -104,6 +104,8 @@ def lib():
             "kr_rope_kv_append": (i32, [vp, vp, vp, vp, vp, u32, u32, u32, u32, vp, vp, u32, vp]),
             "kr_attention_decode": (i32, [vp, vp, vp, vp, u32, u32, u32, u32, u32, vp, vp]),
             "kr_argmax": (i32, [vp, u32, u32, vp, vp]),
+            "kr_argmax_workspace_bytes": (sz, [u32, u32]),
+            "kr_argmax_ws": (i32, [vp, u32, u32, vp, vp, sz, vp]),
             "kr_attention_workspace_bytes": (sz, [u32, u32, u32, u32]),
             "kr_rmsnorm_q4_qkv": (i32, [vp, vp, ctypes.c_float, M, M, M, vp, vp, vp, u32, vp, vp, vp, i32, vp, vp]),
             "kr_rmsnorm_q4_mlp_workspace_bytes": (sz, [u32, u32, u32]),
@@ -508,11 +510,24 @@ def rope_attention_q4_out(q, k, v, cos_sin, positions, q_heads, kv_heads, head_d
     return h
 
 
-def argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+def argmax_workspace(rows: int, n: int, device="cuda") -> torch.Tensor:
+    """Device workspace of argmax(..., workspace=) (per-block partial results)."""
+    nbytes = int(lib().kr_argmax_workspace_bytes(rows, n))
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None,
+           stream=None) -> torch.Tensor:
+    """Greedy argmax per row (ties to the lowest index, NaN never taken): kr_argmax, or with a workspace
+    (argmax_workspace) kr_argmax_ws, which spreads each row over several blocks (same result)."""
     rows, n = logits.shape
     if out is None:
         out = torch.empty(rows, dtype=torch.int32, device=logits.device)
-    _check(lib().kr_argmax(_ptr(logits), rows, n, _ptr(out), _stream(stream)))
+    if workspace is None:
+        _check(lib().kr_argmax(_ptr(logits), rows, n, _ptr(out), _stream(stream)))
+    else:
+        _check(lib().kr_argmax_ws(_ptr(logits), rows, n, _ptr(out), _ptr(workspace), workspace.numel(),
+                                  _stream(stream)))
     return out
 
 

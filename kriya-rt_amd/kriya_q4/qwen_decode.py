@@ -32,8 +32,9 @@ from typing import List
 
 import torch
 
-from . import (ACT_SWIGLU, DTYPE_BF16, DTYPE_F32, Q4Matrix, argmax, attention_q4_out_workspace, embedding, lib,
-               q4_linear, rmsnorm, rmsnorm_mlp, rmsnorm_mlp_workspace, rmsnorm_qkv, rope_attention_q4_out)
+from . import (ACT_SWIGLU, DTYPE_BF16, DTYPE_F32, Q4Matrix, argmax, argmax_workspace, attention_q4_out_workspace,
+               embedding, lib, q4_linear, rmsnorm, rmsnorm_mlp, rmsnorm_mlp_workspace, rmsnorm_qkv,
+               rope_attention_q4_out)
 
 
 @dataclasses.dataclass(frozen=True)
@@ -143,7 +144,8 @@ class QwenQ4Decoder:
         self.k = torch.empty((batch, kv), dtype=torch.bfloat16, device=device)
         self.v = torch.empty_like(self.k)
         self.logits = torch.empty((batch, c.vocab), dtype=torch.float32, device=device)
-        self.next = torch.empty(batch, dtype=torch.int32, device=device)
+        self.next = self.tokens  # greedy: the argmax writes the token the next step embeds
+        self.argmax_ws = argmax_workspace(batch, c.vocab, device=device)
         self.ws = rmsnorm_mlp_workspace(batch, c.hidden, c.inter, device=device)
         self.attn_ws = attention_q4_out_workspace(batch, c.q_heads, c.head_dim, self.max_ctx, device=device)
 
@@ -186,6 +188,5 @@ class QwenQ4Decoder:
                         stream=stream)
         rmsnorm(self.h, self.ln_f, c.eps, out=self.x, stream=stream)
         q4_linear(self.embed, self.x, y=self.logits, out_dtype=DTYPE_F32, stream=stream)
-        argmax(self.logits, out=self.next, stream=stream)
-        self.tokens.copy_(self.next)  # greedy: the next step embeds this step's token
+        argmax(self.logits, out=self.next, workspace=self.argmax_ws, stream=stream)
         return self.next

@@ -92,6 +92,24 @@ def test_gate_up_and_mlp_argument_checks(kq):
     assert rc == kq.KR_E_INVALID  # an f32 residual needs a separate bf16 input
 
 
+def test_argmax_workspace_sizes_and_checks(kq):
+    """kr_argmax_ws: the workspace holds one (value, index) pair per block of a row; the parts per row
+    give every block at least 1024 logits and about 512 blocks in all; short workspaces are refused."""
+    L = kq.lib()
+    assert L.kr_argmax_workspace_bytes(0, 151936) == 0
+    for rows, n, parts in ((1, 151936, 148), (16, 151936, 32), (3, 4097, 4), (1, 100, 1), (600, 151936, 1)):
+        need = L.kr_argmax_workspace_bytes(rows, n)
+        assert need % 256 == 0 and need >= rows * parts * 8 and need < rows * parts * 8 + 256, (rows, n, need)
+    need = L.kr_argmax_workspace_bytes(16, 151936)
+    logits, out = 0x40000, 0x50000
+    assert L.kr_argmax_ws(logits, 16, 151936, out, 0x60000, need - 1, None) == kq.KR_E_WORKSPACE
+    assert L.kr_argmax_ws(logits, 16, 151936, out, None, need, None) == kq.KR_E_WORKSPACE
+    assert L.kr_argmax_ws(logits, 16, 151936, out, 0x60004, need, None) == kq.KR_E_ALIGN
+    assert L.kr_argmax_ws(None, 16, 151936, out, 0x60000, need, None) == kq.KR_E_INVALID
+    assert L.kr_argmax_ws(logits, 16, 0, out, 0x60000, need, None) == kq.KR_E_SHAPE
+    assert L.kr_argmax_ws(logits, 0, 151936, out, None, 0, None) == 0
+
+
 def test_format_argument_checks(kq):
     L = kq.lib()
     assert L.kr_q4_from_blocks36(0x1000, 4, 100, 0x2000, 0x3000, 0x4000, None) == kq.KR_E_SHAPE

@@ -208,14 +208,22 @@ def test_rmsnorm_fused_qkv_and_mlp(kq, m):
                      what=f"fused mlp m={m}")
 
 
-def test_argmax_ties_and_nan(kq):
-    case("argmax")
+def _argmax_dev(kq, x, split):
+    """kq.argmax of a host array: one block per row (kr_argmax) or split over blocks (kr_argmax_ws)."""
+    xd = torch.from_numpy(x).cuda()
+    ws = kq.argmax_workspace(x.shape[0], x.shape[1]) if split else None
+    return kq.argmax(xd, workspace=ws).cpu().numpy()
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_argmax_ties_and_nan(kq, split):
+    case(f"argmax split={split}")
     x = np.random.default_rng(3).standard_normal((4, 1000)).astype(np.float32)
     x[1, 10] = x[1, 700] = 50.0          # tie -> lowest index
     x[2, :] = np.nan
     x[2, 999] = -1.0                      # NaN never wins
     x[3, 123] = np.inf
-    got = kq.argmax(torch.from_numpy(x).cuda()).cpu().numpy()
+    got = _argmax_dev(kq, x, split)
     assert got.tolist() == [int(np.argmax(x[0])), 10, 999, 123]
 
 
@@ -227,9 +235,10 @@ def _argmax_ref(row):
     return int(np.flatnonzero(valid & (row == row[valid].max()))[0])
 
 
+@pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("n", [151936, 1001, 8])
-def test_argmax_quads_and_vocab_rows(kq, n):
-    case(f"argmax n={n}: ties inside and across float4 quads, NaN next to the max, -inf rows")
+def test_argmax_quads_and_vocab_rows(kq, n, split):
+    case(f"argmax n={n} split={split}: ties inside and across float4 quads, NaN next to the max, -inf rows")
     rng = np.random.default_rng(n)
     x = rng.standard_normal((8, n)).astype(np.float32)
     x[1, 5] = x[1, 6] = 60.0                          # tie inside one quad
@@ -241,9 +250,45 @@ def test_argmax_quads_and_vocab_rows(kq, n):
     x[6, :] = -np.inf
     x[6, 3] = np.nan
     x[7, n - 1] = np.inf
-    got = kq.argmax(torch.from_numpy(x).cuda()).cpu().numpy()
+    got = _argmax_dev(kq, x, split)
     want = [_argmax_ref(r) for r in x]
     assert got.tolist() == want
+
+
+@pytest.mark.parametrize("rows,n", [(1, 151936), (16, 151936), (3, 4097), (2, 1027), (1, 2048)])
+def test_argmax_split_block_edges(kq, rows, n):
+    """kr_argmax_ws spreads a row over argmax_parts blocks: maxima tied across a block border,
+    NaN runs covering whole blocks, the winner in the last (ragged) block; the same index as
+    kr_argmax and as the reference rule (first maximum, NaN never taken)."""
+    case(f"argmax split rows={rows} n={n}")
+    parts = int(kq.lib().kr_argmax_workspace_bytes(rows, n)) // 8 // rows  # >= the true count
+    rng = np.random.default_rng(rows * 100003 + n)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    per = -(-n // max(1, parts))
+    for r in range(rows):
+        kind = r % 4
+        if kind == 0 and per < n:      # equal maxima on both sides of a block border
+            b = min(per * (1 + r % max(1, parts - 1)), n - 1)
+            x[r, b - 1] = x[r, b] = 70.0
+        elif kind == 1:                # NaN over the first half, the max in the last element
+            x[r, : n // 2] = np.nan
+            x[r, n - 1] = 80.0
+        elif kind == 2:                # all -inf but one NaN and a later -inf run
+            x[r, :] = -np.inf
+            x[r, 0] = np.nan
+        else:                          # the max repeated in every block: the first wins
+            x[r, ::max(1, per // 2)] = 90.0
+    want = [_argmax_ref(row) for row in x]
+    got_split = _argmax_dev(kq, x, True)
+    got_one = _argmax_dev(kq, x, False)
+    assert got_split.tolist() == want
+    assert got_one.tolist() == want
+    # logits starting off a 16-byte boundary take the element path
+    if n % 4 == 0:
+        buf = torch.from_numpy(np.concatenate([np.zeros(1, np.float32), x.reshape(-1)])).cuda()
+        view = buf[1:].view(rows, n)
+        got = kq.argmax(view, workspace=kq.argmax_workspace(rows, n)).cpu().numpy()
+        assert got.tolist() == want
 
 
 @pytest.mark.parametrize("batch", [1, 3])
