@@ -70,9 +70,11 @@ int kr_rmsnorm_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr
 /* RoPE + KV append + decode attention in two launches: the results of
  * kr_rope_kv_append followed by kr_attention_decode (up to f32 summation
  * order), except that q is only read (its rotated copy is not written back).
- * The context is split into 16-position slices; one block takes a slice of one
- * sequence for one kv head and all the query heads that share it (GQA), and a
- * second launch merges the slices in a fixed order.
+ * The context is split into slices of 16 positions (64 with head_dim 128 when
+ * the 64-position slices still give a block per compute unit,
+ * KR_OPT_ATTN_SLICE64); one block takes a slice of one sequence for one kv head
+ * and all the query heads that share it (GQA), and a second launch merges the
+ * slices in a fixed order.
  * workspace: kr_attention_workspace_bytes(batch, q_heads, head_dim, max_ctx)
  * bytes, 16-byte aligned (per-slice partial sums); calls sharing a workspace
  * must not overlap in time.

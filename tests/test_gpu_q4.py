@@ -284,6 +284,35 @@ def test_gemv_tokens_linear(kq, m, n, k):
         assert np.max(np.abs(y - y2)) <= 1e-4 * rms(want)
 
 
+@pytest.mark.parametrize("m", [5, 8, 13, 16])
+@pytest.mark.parametrize("n,k", [(300, 11008), (77, 4160)])
+def test_linear_few_tokens_long_k(kq, m, n, k):
+    """5 <= m <= 16 tokens over k > 2048 without a workspace (kr_q4_linear has none for the few-token
+    kernel's split K): the token GEMV in chunks of at most 4 tokens.  All four epilogues against the
+    oracle; every token's row as a call with that token alone gives it (bit for bit)."""
+    s = synth()
+    case(f"linear few tokens long k m={m} n={n} k={k}")
+    wq = s.q4_weight(n, k, 140 + m)
+    x = s.bf16_normal((m, k), 150 + m)
+    want = O.q4_matmul(O.Q4Planar(*wq), x)
+    wd, xd = q4_dev(kq, wq), dev_bf16(x)
+    y = kq.q4_linear(wd, xd, out_dtype=kq.DTYPE_F32)
+    assert_rms_close(y.cpu().numpy(), want, what=f"m={m} f32")
+    for t in (0, m // 2, m - 1):
+        yt = kq.q4_linear(wd, xd[t:t + 1].contiguous(), out_dtype=kq.DTYPE_F32)
+        assert torch.equal(yt[0].view(torch.int32), y[t].view(torch.int32)), f"token {t}"
+    yb = kq.q4_linear(wd, xd, out_dtype=kq.DTYPE_BF16)
+    assert_bf16_rounded_close(host_bits(yb), want, rms(want), what=f"m={m} bf16")
+    base = s.f32_normal((m, n), 160 + m)
+    acc32 = torch.from_numpy(base.copy()).cuda()
+    kq.q4_linear(wd, xd, y=acc32, accumulate=True)
+    assert_rms_close(acc32.cpu().numpy() - base, want, what=f"m={m} acc f32")
+    base_b = s.bf16_normal((m, n), 170 + m)
+    accb = dev_bf16(base_b).clone()
+    kq.q4_linear(wd, xd, y=accb, accumulate=True)
+    assert_bf16_rounded_close(host_bits(accb), O.bf16_to_f32(base_b) + want, rms(want), what=f"m={m} acc bf16")
+
+
 @pytest.mark.parametrize("m", [2, 3, 4])
 @pytest.mark.parametrize("n,k", [(500, 2048), (37, 1408), (11008, 2048)])
 def test_gemv_tokens_gate_up(kq, m, n, k):
