@@ -283,12 +283,19 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     // requested the first tile's words) the conversion and LDS stores.
     // Loads are unconditional (dead units re-read row `base`, unit 0) and
     // zeroed after, so that no branch splits the batch of loads.
+    // Unit s of a thread: row 2 wave + s / 4, column block lane + 64 (s % 4) -- a wave holds two whole
+    // rows, so the RMSNorm below needs no other wave.
+    static_assert(kStage == 8 && kUnits == 4 * 64 && NW * 2 == 16, "two 256-unit rows per wave");
+    auto unit_of = [&](int s, uint32_t &r, uint32_t &u) {
+        r = 2u * (uint32_t)wave + ((uint32_t)s >> 2);
+        u = (uint32_t)lane + 64u * ((uint32_t)s & 3u);
+    };
     u32x4 raw[MG][kStage];  // [row group]
     auto stage_load = [&](u32x4(&rw)[kStage], uint32_t base, uint32_t rows) {
 #pragma unroll
         for (int s = 0; s < kStage; ++s) {
-            const uint32_t idx = (uint32_t)tid + (uint32_t)s * (NW * 64);
-            const uint32_t r = idx / kUnits, u = idx % kUnits;
+            uint32_t r, u;
+            unit_of(s, r, u);
             const bool live = r < rows && u < npieces * 16;
             uint32_t xr = base + (live ? r : 0u);
             if constexpr (kGrouped) {
@@ -300,8 +307,8 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     auto stage_store = [&](const u32x4(&rw)[kStage], uint32_t rows) {
 #pragma unroll
         for (int s = 0; s < kStage; ++s) {
-            const uint32_t idx = (uint32_t)tid + (uint32_t)s * (NW * 64);
-            const uint32_t r = idx / kUnits, u = idx % kUnits;
+            uint32_t r, u;
+            unit_of(s, r, u);
             const bool live = r < rows && u < npieces * 16;
             const u32x4 z = {0, 0, 0, 0};
             xs[xs_index<kUnits>(r, u)] = x_unit(live ? rw[s] : z);
@@ -311,49 +318,51 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     // LDS-only barrier: the weight prefetch stays in flight across it (a
     // barrier with a memory fence would wait for every outstanding load).
     auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
-    // RMSNorm of the staged rows (dense mode, the whole row in this slab):
-    // every unit of a thread is column block u = tid % kUnits of rows
-    // tid / kUnits + 2 s, so one ln_w unit serves all of them.  Per-row sums of
-    // squares: wave sums, then the four waves of a row parity in order.
-    // (s_ss and s_scale live in the reduction buffer, unused until the first tile)
-    float (*s_ss)[4] = reinterpret_cast<float (*)[4]>(&red[0][0][0][0][0]);
-    float *s_scale = &red[1][0][0][0][0];
+    // RMSNorm of the staged rows (dense mode, the whole row in this slab), kr_rmsnorm's arithmetic and
+    // order: per 8-column unit a sequential sum of squares, per 64 units (lanes) the wave tree, the four
+    // quarters of the row added in order; then bf16(x * (1 / sqrt(mean + eps)) * w).  The wave holds its
+    // two rows whole, so every lane forms the scales itself: no LDS, no barrier.
     auto norm_x = [&](u32x4(&rw)[kStage], uint32_t rows) {
-        static_assert(NW * 64 == 2 * kUnits, "two rows per staging round");
-        const uint32_t u = (uint32_t)tid % kUnits, r0 = (uint32_t)tid / kUnits;
-        const bool ulive = u < npieces * 16;
-        const u32x4 wl = *reinterpret_cast<const u32x4 *>(a.ln_w + k0 + 8 * (ulive ? u : 0u));
+        u32x4 wl[4];
 #pragma unroll
-        for (int st = 0; st < kStage; ++st) {
-            const uint32_t r = r0 + 2u * (uint32_t)st;
-            float ss = 0.0f;
-            if (ulive && r < rows) {
-                const uint32_t X[4] = {rw[st].x, rw[st].y, rw[st].z, rw[st].w};
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t u = (uint32_t)lane + 64u * (uint32_t)q;
+            wl[q] = *reinterpret_cast<const u32x4 *>(a.ln_w + k0 + 8 * (u < npieces * 16 ? u : 0u));
+        }
+        float scale[2];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float lo = __uint_as_float(X[i] << 16), hi = __uint_as_float(X[i] & 0xFFFF0000u);
-                    ss = fmaf(lo, lo, ss);
-                    ss = fmaf(hi, hi, ss);
+        for (int h = 0; h < 2; ++h) {
+            float tot = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t r, u;
+                unit_of(4 * h + q, r, u);
+                float ss = 0.0f;
+                if (u < npieces * 16 && r < rows) {
+                    const u32x4 v = rw[4 * h + q];
+                    const uint32_t X[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float lo = __uint_as_float(X[i] << 16), hi = __uint_as_float(X[i] & 0xFFFF0000u);
+                        ss = fmaf(lo, lo, ss);
+                        ss = fmaf(hi, hi, ss);
+                    }
                 }
+                ss = wave_total(ss, lane);
+                tot = q == 0 ? ss : tot + ss;
             }
-            ss = wave_total(ss, lane);
-            if (lane == 0) s_ss[r][wave & 3] = ss;
+            scale[h] = 1.0f / sqrtf(tot / (float)K + a.eps);
         }
-        lds_barrier();
-        if (tid < 16) {
-            const float tot = ((s_ss[tid][0] + s_ss[tid][1]) + s_ss[tid][2]) + s_ss[tid][3];
-            s_scale[tid] = 1.0f / sqrtf(tot / (float)K + a.eps);
-        }
-        lds_barrier();
-        const uint32_t W[4] = {wl.x, wl.y, wl.z, wl.w};
 #pragma unroll
         for (int st = 0; st < kStage; ++st) {
-            const float scale = s_scale[r0 + 2u * (uint32_t)st];
+            const float sc = scale[st >> 2];
+            const u32x4 wq = wl[st & 3];
+            const uint32_t W[4] = {wq.x, wq.y, wq.z, wq.w};
             uint32_t X[4] = {rw[st].x, rw[st].y, rw[st].z, rw[st].w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float lo = __uint_as_float(X[i] << 16) * scale * __uint_as_float(W[i] << 16);
-                const float hi = __uint_as_float(X[i] & 0xFFFF0000u) * scale * __uint_as_float(W[i] & 0xFFFF0000u);
+                const float lo = __uint_as_float(X[i] << 16) * sc * __uint_as_float(W[i] << 16);
+                const float hi = __uint_as_float(X[i] & 0xFFFF0000u) * sc * __uint_as_float(W[i] & 0xFFFF0000u);
                 X[i] = pack_bf16_rne(lo, hi);
             }
             rw[st] = u32x4{X[0], X[1], X[2], X[3]};
