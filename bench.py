@@ -94,21 +94,29 @@ def chain_time_per_launch(torch, fn, n, reps=3):
     """Average duration of one launch of fn(i): n eager launches fn(0) .. fn(n - 1) are queued behind a bounded spin
     kernel and bracketed by two HIP events on the launch stream; the median over `reps` chains of elapsed / n.
     rocprofv3 --kernel-trace reports the same average duration for the kernel (within ~1 %), whereas replays of a
-    HIP graph of the chain run a few per cent apart from it.  Returns (seconds per launch, starved) where starved is
-    True if a chain's hold ended before the host had queued the whole chain (then host gaps may be included)."""
+    HIP graph of the chain run a few per cent apart from it.  A chain whose hold ended before the host had queued
+    it is run again behind a hold twice as long (up to 16x: a profiler slows the host's launches several-fold).
+    Returns (seconds per launch, starved) where starved is True if a chain was still not fully queued when its
+    hold ended (then host gaps may be included)."""
     for i in range(min(n, 3)):
         fn(i)
     torch.cuda.synchronize()
     times, starved = [], False
+    hold = HOLD_CYCLES * max(1, -(-n // CHAIN_LAUNCHES))
     for _ in range(reps):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda._sleep(HOLD_CYCLES * max(1, -(-n // CHAIN_LAUNCHES)))
-        a.record()
-        for i in range(n):
-            fn(i)
-        b.record()
-        starved |= a.query()  # the hold already ended: the GPU may have waited for the host
-        torch.cuda.synchronize()
+        for attempt in range(5):  # a slow host (e.g. under a profiler) gets a longer hold, up to 16x
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(hold)
+            a.record()
+            for i in range(n):
+                fn(i)
+            b.record()
+            short = a.query()  # the hold already ended: the GPU may have waited for the host
+            torch.cuda.synchronize()
+            if not short or attempt == 4:
+                break
+            hold *= 2
+        starved |= short
         times.append(a.elapsed_time(b) * 1e-3 / n)
     return float(np.median(times)), starved
 
