@@ -95,14 +95,14 @@ const char *kr_last_error(void);
                                            MoE launches take twice this)                  */
 #define KR_OPT_PREFILL_KERNEL 7         /* m > 16: 0 register-dequant (default), 1 tiled, 2 register-dequant
                                            with 64-column steps (0 takes 128 where k allows) */
-#define KR_OPT_GEMV_LONG_ROWS 8         /* k > 4096 rows per long-row block: 4, 8 (default), 16; 0 split-K */
+#define KR_OPT_GEMV_LONG_ROWS 8         /* k > 4096 rows per long-row block: 4 (default), 8, 16; 0 split-K */
 #define KR_OPT_GEMV_TOKENS 9            /* 2 <= m <= 4: 1 (default) the GEMV kernels take all tokens per
                                            unpacked word (k <= 2048, or k <= 16384 without gate/up);
                                            0 the few-token MFMA kernel */
 #define KR_OPT_MOE_GEMV 10              /* kr_q4_moe_experts with tokens * topk <= 16: 1 (default) one GEMV
                                            per (expert, token) pair, 0 the grouped MFMA kernel */
 #define KR_OPT_GEMV_LONG_GROUPS 11      /* long-row kernel: row groups of 512 threads per block, each
-                                           taking rows / groups of the block's rows: 1 or 2 (default) */
+                                           taking rows / groups of the block's rows: 1 (default) or 2 */
 #define KR_OPT_SPLITK_TICKETS 12        /* kr_q4_mlp at 2 <= m <= 16: 1 (default) the down projection's
                                            K split is reduced by the last block of each run (one launch),
                                            0 by a second launch */

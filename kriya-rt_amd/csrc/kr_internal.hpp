@@ -33,9 +33,9 @@ struct Tuning {
                                        // grouped MoE launches take twice this
     int prefill_kernel = 0;            // m > 16: 0 = register-dequant prefill kernel,
                                        // 1 = LDS-dequant tiled kernel
-    int gemv_long_rows = 8;            // k > 4096: rows per block of the long-row kernels (4, 8, 16);
+    int gemv_long_rows = 4;            // k > 4096: rows per block of the long-row kernels (4, 8, 16);
                                        // 0 = split-K block kernel
-    int gemv_long_groups = 2;          // long-row kernel: row groups of 512 threads per block (1, 2)
+    int gemv_long_groups = 1;          // long-row kernel: row groups of 512 threads per block (1, 2)
     int gemv_tokens = 1;               // 2 <= m <= 4: GEMV kernels over the tokens (1) or the few-token
                                        // MFMA kernel (0)
     int moe_gemv = 1;                  // MoE with <= 16 assignments: routed GEMV (1) or grouped MFMA kernel (0)
