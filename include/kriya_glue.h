@@ -50,9 +50,11 @@ int kr_attention_decode(const uint16_t *q, const uint16_t *k_cache, const uint16
  * the Q4 call, up to the f32 summation order of mean(x^2).
  *
  * qkv(rmsnorm(h)): arguments as kr_q4_qkv, with h bf16 [m, k] and ln_weight bf16
- * [k].  m == 1 with k <= 4096 is one launch: every wave of the GEMV holds all of
- * h and normalises its own chunks.  Otherwise the norm goes to xnorm (bf16
- * [m, k], 16-byte aligned; may be NULL when m == 1 and k <= 4096) first. */
+ * [k].  One launch when m == 1 with k <= 4096 (each block of the GEMV normalises
+ * h into its LDS) and for the few-token kernel (2 <= m <= 63 with k <= 2048;
+ * each wave normalises the rows it stages); xnorm is then not written.
+ * Otherwise the norm goes to xnorm (bf16 [m, k], 16-byte aligned; may be NULL
+ * in the one-launch cases) first. */
 int kr_rmsnorm_q4_qkv(const uint16_t *h, const uint16_t *ln_weight, float eps, const kr_q4_matrix *q,
                       const kr_q4_matrix *k, const kr_q4_matrix *v, const uint16_t *q_bias, const uint16_t *k_bias,
                       const uint16_t *v_bias, uint32_t m, void *q_out, void *k_out, void *v_out, int out_dtype,
