@@ -69,3 +69,24 @@ def test_full_size_inputs_match_fixture():
     assert sorted(got) == sorted(want)
     bad = [name for name in want if got[name] != want[name]]
     assert not bad, f"regenerated inputs differ from the fixture: {bad}"
+
+
+@pytest.mark.gpu
+def test_gpu_resident_inputs_match_fixture():
+    """On the GPU box: every seeded input regenerated there, uploaded to HBM as bench.py uploads it and read
+    back, has the fixture's SHA-256 (the bytes the timed kernels read are the ones pinned here)."""
+    import hashlib
+
+    import torch
+
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    with open(os.path.join(GOLDEN, "input_sha256.json")) as f:
+        want = json.load(f)
+    gen = _generator()
+    for name, arrays in gen.inputs():
+        h = hashlib.sha256()
+        for a in arrays:
+            dev = torch.from_numpy(np.ascontiguousarray(a).view(np.uint8)).cuda()
+            h.update(dev.cpu().numpy().tobytes())
+            del dev
+        assert h.hexdigest() == want[name], name
