@@ -194,6 +194,33 @@ def bench_mlp(kq, torch, synth, B, copies, steps, warmup):
     return out
 
 
+def bench_mlp_tp_share(kq, torch, synth, B, tp, copies, steps, warmup):
+    """One GPU's share of config 1's MLP under tp-way tensor parallelism: gate/up rows [0, I/tp) (column-
+    parallel) and the down projection's K columns [0, I/tp) (row-parallel, whole 64-groups), the share's f32
+    partial [B, H] accumulated into a buffer the all-reduce would sum.  Exactly `steps` steps in one graph, as
+    the headline; the all-reduce itself is not run (one GPU)."""
+    H, I = synth.HIDDEN, synth.INTER
+    Is = I // tp
+    assert Is % 64 == 0, "shards must be whole 64-groups"
+    g, u, d = synth.q4_weight(I, H, 1001), synth.q4_weight(I, H, 1002), synth.q4_weight(H, I, 1003)
+    rows = lambda p: tuple(np.ascontiguousarray(a[:Is]) for a in p)  # noqa: E731
+    cols = (np.ascontiguousarray(d[0][:, :Is // 8]), np.ascontiguousarray(d[1][:, :Is // 64]),
+            np.ascontiguousarray(d[2][:, :Is // 64]))
+    rot = Rotation(kq, torch, [rows(g), rows(u), cols], copies)
+    x = torch.from_numpy(synth.bf16_normal((B, H), 1010 + B).view(np.int16)).cuda().view(torch.bfloat16)
+    part = torch.zeros((B, H), dtype=torch.float32, device="cuda")
+    ws = kq.mlp_workspace(B, H, Is)
+
+    def step(i):
+        gs, us, ds = rot.sets[i % len(rot)]
+        kq.mlp(gs, us, ds, part, x=x, workspace=ws)
+
+    t = graph_time_exact(torch, step, steps, warmup)
+    alg = 3 * Q4_BYTES(Is, H) + 2 * B * H + 2 * 4 * B * H  # weights + x + the f32 partial read and written
+    return {"tp": tp, "B": B, "gate_up_rows": Is, "down_k": Is, "step_us": round(t * 1e6, 3),
+            "alg_bytes": alg, "gbs": round(alg / t / 1e9, 1), "frac_hbm": round(alg / t / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def stream_floor(kq, torch, nbytes, copies, steps, warmup):
     """Seconds per plain read of nbytes (kr_stream_read: one 16-byte non-temporal load per thread) over
     `copies` rotating buffers, timed like the kernels: the floor for a read of that size on this GPU."""
@@ -545,6 +572,9 @@ def main():
                                    "tok_s": round(B / r["s_per_step"], 1),
                                    "kernels_us": {"gate_up_act": round(gu * 1e6, 3),
                                                   "down_acc (step - gate_up)": round((r["s_per_step"] - gu) * 1e6, 3)}}
+        log("cfg1 one GPU's share under 4-way tensor parallelism")
+        extra["cfg1_tp4_share"] = {f"B{B}": bench_mlp_tp_share(kq, torch, synth, B, 4, args.copies * 4,
+                                                                 args.steps, args.warmup) for B in (1, 16)}
         log("cfg2 prefill M=512")
         extra["cfg2_prefill_M512"] = bench_prefill_cfg2(kq, torch, synth, 24, args.steps)  # 24 x 43.4 MB
         log("cfg4 MoE")

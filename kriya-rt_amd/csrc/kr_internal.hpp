@@ -227,7 +227,8 @@ hipError_t launch_moe_combine(const float *d, const float *w, uint32_t T, uint32
 uint32_t skinny_ksplit(uint32_t k);
 // True when one block of the grouped kernel covers rows of k columns (no K split).
 bool skinny_grouped_fits(uint32_t k);
-// The few-token kernel needs k % 128 == 0 and 4-byte aligned scales/biases.
+// The few-token kernel needs k % 64 == 0, and 4-byte aligned scales/biases when k % 128 == 0
+// (an odd group count loads them 2 bytes at a time); its grouped (MoE) mode needs k % 128 == 0.
 bool skinny_supported(const Q4Mat &w);
 
 // ---- embedding and end-to-end glue (e2e_glue.hip)

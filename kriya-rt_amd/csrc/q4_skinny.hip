@@ -112,10 +112,15 @@ __device__ __forceinline__ uint32_t xs_index(uint32_t r, uint32_t u) {
 // kernel's pace (measured: two dummy loads per tile cost 0.7 us of 13.8 at cfg1 B = 16 gate/up).
 // D: register buffers of tile words, i.e. D - 1 tiles in flight while one is multiplied (2, or 3
 // for dense runs of at least 6 tiles: the launcher's choice).
-template <bool kGateUp, bool kGrouped, int MG, bool kPre, int D>
+// kOdd: K is an odd number of 64-groups (K % 128 == 64; dense mode): the last piece of the last slab
+// holds one group.  Its other half re-reads the live half's words (in the row, never past it), meets
+// zero X and a zero scale and bias, and the scale/bias pairs come in two 2-byte loads (a row's pairs
+// are not 4-byte aligned when K / 64 is odd).
+template <bool kGateUp, bool kGrouped, int MG, bool kPre, int D, bool kOdd>
 __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_eu(kGrouped ? 4 : 2))) void q4_skinny_kernel(
     SkinnyArgs a) {
     static_assert(MG == 1 || (MG == 2 && !kGrouped), "two row groups in dense mode only");
+    static_assert(!(kOdd && kGrouped), "odd group counts in dense mode only");
     static_assert(!(kPre && (kGrouped || kGateUp)), "bias and accumulation: dense plain tiles only");
     static_assert(D == 2 || (D == 3 && !kGrouped), "a deeper ring in dense mode only");
     static_assert(!kPre || D == 2, "epilogue operands with one tile in flight only");
@@ -134,7 +139,9 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
     const uint32_t K = a.k;
     const uint32_t slab = blockIdx.x % a.ksplit;
     const uint32_t k0 = slab * (uint32_t)kSlabCols;
-    const uint32_t npieces = min((uint32_t)(NW * KW), (K - k0) >> 7);  // live pieces of the slab (K % 128 == 0)
+    // live pieces of the slab (the last one half when K % 128 == 64) and live 8-column X units
+    const uint32_t npieces = min((uint32_t)(NW * KW), (K - k0 + 127) >> 7);
+    const uint32_t kunits = min((uint32_t)(NW * KW * 16), (K - k0) >> 3);
     const uint32_t p0 = (uint32_t)wave * KW;                           // this wave's first piece
     const uint32_t kMask = opq_s(0x000F000Fu);
     const uint32_t kMagic = opq_v(0x43004300u);  // bf16 128.0 in both halves
@@ -257,7 +264,11 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         for (int i = 0; i < KW; ++i) {
             uint32_t p = p0 + (uint32_t)i;
             p = p < npieces ? p : npieces - 1;
-            wv[b][i] = ld_stream(src + 4 * p + g);
+            uint32_t gw = (uint32_t)g;
+            if constexpr (kOdd) {  // the half piece: lane groups 2, 3 re-read groups 0, 1 of it
+                if (k0 + 128u * p + 32u * gw >= K) gw -= 2u;
+            }
+            wv[b][i] = ld_stream(src + 4 * p + gw);
         }
         // The scales and biases of the wave's two pieces in one load: lane group g reads the bf16
         // pair (groups 2p, 2p + 1) of piece p = p0 + (g >> 1), scales for even g, biases for odd g
@@ -266,7 +277,13 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
             uint32_t p = p0 + ((uint32_t)g >> 1);
             p = p < npieces ? p : npieces - 1;
             const uint16_t *base = ((uint32_t)g & 1u) ? bi_base : sc_base;
-            sb[b] = reinterpret_cast<const uint32_t *>(base + row * kg + (k0 >> 6))[p];
+            if constexpr (kOdd) {  // groups 2p, 2p + 1 (clamped to the row's last; tile_mma masks it)
+                const uint16_t *rg = base + row * kg;
+                const uint32_t i0 = (k0 >> 6) + 2u * p, i1 = min(i0 + 1u, kg - 1u);
+                sb[b] = (uint32_t)rg[i0] | ((uint32_t)rg[i1] << 16);
+            } else {
+                sb[b] = reinterpret_cast<const uint32_t *>(base + row * kg + (k0 >> 6))[p];
+            }
         }
     };
     // The epilogue's operands (when the launch has any) are requested first: loads complete in
@@ -296,7 +313,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         for (int s = 0; s < kStage; ++s) {
             uint32_t r, u;
             unit_of(s, r, u);
-            const bool live = r < rows && u < npieces * 16;
+            const bool live = r < rows && u < kunits;
             uint32_t xr = base + (live ? r : 0u);
             if constexpr (kGrouped) {
                 if (a.x_div) xr = a.sorted[xr] / a.x_div;
@@ -309,7 +326,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         for (int s = 0; s < kStage; ++s) {
             uint32_t r, u;
             unit_of(s, r, u);
-            const bool live = r < rows && u < npieces * 16;
+            const bool live = r < rows && u < kunits;
             const u32x4 z = {0, 0, 0, 0};
             xs[xs_index<kUnits>(r, u)] = x_unit(live ? rw[s] : z);
         }
@@ -327,7 +344,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t u = (uint32_t)lane + 64u * (uint32_t)q;
-            wl[q] = *reinterpret_cast<const u32x4 *>(a.ln_w + k0 + 8 * (u < npieces * 16 ? u : 0u));
+            wl[q] = *reinterpret_cast<const u32x4 *>(a.ln_w + k0 + 8 * (u < kunits ? u : 0u));
         }
         float scale[2];
 #pragma unroll
@@ -338,7 +355,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
                 uint32_t r, u;
                 unit_of(4 * h + q, r, u);
                 float ss = 0.0f;
-                if (u < npieces * 16 && r < rows) {
+                if (u < kunits && r < rows) {
                     const u32x4 v = rw[4 * h + q];
                     const uint32_t X[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -431,7 +448,13 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
         for (int i = 0; i < KW; ++i) {
             // past the slab: the re-read words meet zero X; zero scales keep the products at 0
             const bool live = p0 + (uint32_t)i < npieces;
-            const uint32_t sv = live ? spp[i] : 0u, bv = live ? bpp[i] : 0u;
+            uint32_t sv = live ? spp[i] : 0u, bv = live ? bpp[i] : 0u;
+            if constexpr (kOdd) {  // the half piece's missing group: zero scale and bias
+                if (k0 + 128u * (p0 + (uint32_t)i) + 64u >= K) {
+                    sv &= 0xFFFFu;
+                    bv &= 0xFFFFu;
+                }
+            }
             // swap words (0, 1) and (2, 3) across the lane halves: [0] holds group 2p, [1] group 2p + 1
             const auto p01 = __builtin_amdgcn_permlane32_swap(wv[b][i].x, wv[b][i].y, false, false);
             const auto p23 = __builtin_amdgcn_permlane32_swap(wv[b][i].z, wv[b][i].w, false, false);
@@ -769,14 +792,14 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) __attribute__((amdgpu_waves_per_
 
 namespace {
 
-template <bool GU, bool G, int MG, bool P, int D>
+template <bool GU, bool G, int MG, bool P, int D, bool O>
 hipError_t launch_d(SkinnyArgs &a, uint32_t nblk, hipStream_t s) {
     const dim3 grid(nblk * a.ksplit), block(kSkinnyWaves * 64);
-    hipLaunchKernelGGL((q4_skinny_kernel<GU, G, MG, P, D>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((q4_skinny_kernel<GU, G, MG, P, D, O>), grid, block, 0, s, a);
     return hipGetLastError();
 }
 
-template <bool GU, bool G, int MG, bool P>
+template <bool GU, bool G, int MG, bool P, bool O>
 hipError_t launch_t(SkinnyArgs &a, uint32_t items, hipStream_t s) {
     // blocks per slab: every CU busy, each block a contiguous run of ceil(items / nblk) tiles
     // grouped (MoE) launches take twice the cap: cfg4 T = 64 is 1.3 % faster at 512 blocks, the dense
@@ -789,15 +812,23 @@ hipError_t launch_t(SkinnyArgs &a, uint32_t items, hipStream_t s) {
     if constexpr (!G && !P) {
         const int depth = tuning().skinny_depth;
         const uint32_t per = (items + nblk - 1) / nblk;
-        if (depth == 3 || (depth == 0 && per >= 6)) return launch_d<GU, G, MG, P, 3>(a, nblk, s);
+        if (depth == 3 || (depth == 0 && per >= 6)) return launch_d<GU, G, MG, P, 3, O>(a, nblk, s);
     }
-    return launch_d<GU, G, MG, P, 2>(a, nblk, s);
+    return launch_d<GU, G, MG, P, 2, O>(a, nblk, s);
+}
+
+// dense launches: the even or the odd group-count kernels
+template <bool GU, int MG, bool P>
+hipError_t launch_dense(SkinnyArgs &a, uint32_t items, hipStream_t s) {
+    return a.k % 128 == 0 ? launch_t<GU, false, MG, P, false>(a, items, s) : launch_t<GU, false, MG, P, true>(a, items, s);
 }
 
 }  // namespace
 
 bool skinny_supported(const Q4Mat &w) {
-    return w.k % 128 == 0 && (uintptr_t)w.sc % 4 == 0 && (uintptr_t)w.bi % 4 == 0;
+    if (w.k == 0 || w.k % 64 != 0) return false;
+    // even group counts load each scale/bias pair as one 4-byte word
+    return w.k % 128 != 0 || ((uintptr_t)w.sc % 4 == 0 && (uintptr_t)w.bi % 4 == 0);
 }
 
 hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s) {
@@ -805,7 +836,7 @@ hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s) {
     if (!skinny_supported(a.w) || (gate_up && !skinny_supported(a.w2))) return hipErrorInvalidValue;
     const bool grouped = a.offsets != nullptr;
     a.ksplit = skinny_ksplit(a.k);
-    if (grouped && a.ksplit != 1) return hipErrorInvalidValue;
+    if (grouped && (a.ksplit != 1 || a.k % 128 != 0)) return hipErrorInvalidValue;
     if (grouped && (a.nmore > 0 || a.ln_w || a.bias || a.accumulate)) return hipErrorInvalidValue;
     if (a.nmore < 0 || a.nmore > 2 || (a.nmore > 0 && (gate_up || a.partial))) return hipErrorInvalidValue;
     if (!grouped && (a.m == 0 || a.m > kSkinnyMaxM)) return hipErrorInvalidValue;
@@ -831,18 +862,20 @@ hipError_t launch_skinny(SkinnyArgs &a, hipStream_t s) {
         pre = a.bias != nullptr || a.accumulate;
         for (int i = 0; i < a.nmore; ++i) pre = pre || a.more[i].bias != nullptr;
     }
-    if (grouped) return gate_up ? launch_t<true, true, 1, false>(a, items, s) : launch_t<false, true, 1, false>(a, items, s);
+    if (grouped)
+        return gate_up ? launch_t<true, true, 1, false, false>(a, items, s)
+                       : launch_t<false, true, 1, false, false>(a, items, s);
     if (gate_up && pre) return hipErrorInvalidValue;  // gate/up launches have neither
     if (a.m > 16) {  // two row groups per launch
-        if (gate_up) return launch_t<true, false, 2, false>(a, items, s);
-        return pre ? launch_t<false, false, 2, true>(a, items, s) : launch_t<false, false, 2, false>(a, items, s);
+        if (gate_up) return launch_dense<true, 2, false>(a, items, s);
+        return pre ? launch_dense<false, 2, true>(a, items, s) : launch_dense<false, 2, false>(a, items, s);
     }
-    if (gate_up) return launch_t<true, false, 1, false>(a, items, s);
-    return pre ? launch_t<false, false, 1, true>(a, items, s) : launch_t<false, false, 1, false>(a, items, s);
+    if (gate_up) return launch_dense<true, 1, false>(a, items, s);
+    return pre ? launch_dense<false, 1, true>(a, items, s) : launch_dense<false, 1, false>(a, items, s);
 }
 
 uint32_t skinny_ksplit(uint32_t k) { return (k + kSlabCols - 1) / kSlabCols; }
 
-bool skinny_grouped_fits(uint32_t k) { return k % 128 == 0 && skinny_ksplit(k) == 1; }
+bool skinny_grouped_fits(uint32_t k) { return k % 128 == 0 && skinny_ksplit(k) == 1; }  // even group counts only
 
 }  // namespace kr
