@@ -189,6 +189,25 @@ int kr_f16_to_bf16(const uint16_t *in, uint16_t *out, size_t count, void *stream
 int kr_q4_linear(const kr_q4_matrix *w, const uint16_t *x, uint32_t m,
                  void *y, int y_dtype, int accumulate, void *stream);
 
+/* The same Q4 linear (encoder.rs:2361-2420, 2497-2536; the same y and the
+ * same accumulate semantics) with a caller workspace.  The workspace lets
+ * 5 <= m rows over a long K (more than 2048 columns, and at m >= 64 few
+ * output tiles) split K over blocks into f32 partials, summed in a fixed
+ * order.  kr_q4_linear has no such buffer: there a few tokens over a long row
+ * take the token GEMV in chunks, and more take the unsplit tiled kernel.
+ * Results are within f32 summation order of kr_q4_linear's, and the same
+ * bits from run to run.
+ * workspace: kr_q4_linear_workspace_bytes(m, w->n, w->k) bytes, 16-byte
+ * aligned, zero-filled once before its first use.  It holds the counters
+ * that pick the block that sums a tile's partials, and every call leaves
+ * them at zero.  Calls sharing a workspace must not overlap in time.  A
+ * workspace sized for (m, n, k) serves every smaller m with the same n and k.
+ * m <= 1 needs none (0 bytes; workspace may be NULL). */
+size_t kr_q4_linear_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
+int kr_q4_linear_ws(const kr_q4_matrix *w, const uint16_t *x, uint32_t m,
+                    void *y, int y_dtype, int accumulate,
+                    void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---- fused gate+up+activation: encoder.rs:2703-2848 (encode_fused_gate_up) ----
  * a[i, j] = act(gate_j . x_i) * (up_j . x_i) for j < gate->n, both dots in f32.
  *   gate, up: same n (intermediate) and k (hidden).

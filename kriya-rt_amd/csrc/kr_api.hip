@@ -613,6 +613,44 @@ static int mlp_down(const kr_q4_matrix *gate, const kr_q4_matrix *down, const ui
     return hip_status(launch_mfma(args, bm, (hipStream_t)stream), "kr_q4_mlp (down)");
 }
 
+// kr_q4_linear with a workspace: [ticket words][split-K partials], the layout of the MLP's down
+// projection (its tickets first, at the same place for every m).
+size_t kr_q4_linear_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
+    if (m <= 1) return 0;
+    return kMlpTicketBytes + partial_bytes(m, n, k, 1);
+}
+
+int kr_q4_linear_ws(const kr_q4_matrix *w, const uint16_t *x, uint32_t m, void *y, int y_dtype, int accumulate,
+                    void *workspace, size_t workspace_bytes, void *stream) {
+    if (int rc = check_matrix(w, "w")) return rc;
+    if (!valid_dtype(y_dtype)) return fail(KR_E_INVALID, "y_dtype %d is not KR_DTYPE_BF16/F32", y_dtype);
+    if (accumulate != 0 && accumulate != 1) return fail(KR_E_INVALID, "accumulate must be 0 or 1");
+    if (m == 0) return ok();
+    if (!x || !y) return fail(KR_E_INVALID, "x/y must be non-NULL");
+    const size_t need = kr_q4_linear_workspace_bytes(m, w->n, w->k);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail(KR_E_WORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    if (need && !aligned(workspace, 16)) return fail(KR_E_ALIGN, "workspace must be 16-byte aligned");
+    const Q4Mat a = to_mat(w);
+    // the shapes that split nothing: as kr_q4_linear (one token, the token GEMV, one K slab)
+    if (m == 1 || (tuning().gemv_tokens && gemv_tokens_supported(m, w->k, false)) || skinny_fits(m, a, false))
+        return kr_q4_linear(w, x, m, y, y_dtype, accumulate, stream);
+    if (!aligned(x, 16)) return fail(KR_E_ALIGN, "x must be 16-byte aligned");
+    if (!aligned(y, dtype_size(y_dtype))) return fail(KR_E_ALIGN, "y is misaligned for its dtype");
+    hipStream_t s = (hipStream_t)stream;
+    float *partial = (float *)((char *)workspace + kMlpTicketBytes);
+    if (skinny_fits(m, a, true))  // 5 <= m <= 63 over more than one K slab
+        return hip_status(run_skinny(a, nullptr, x, m, y, nullptr, w->n, y_dtype, accumulate, 0, partial, s, nullptr,
+                                     0.0f, (uint32_t *)workspace),
+                          "kr_q4_linear_ws");
+    MfmaArgs args = mfma_args(x, m, w->k, y_dtype, accumulate);
+    args.p[0] = problem(a, nullptr, y, nullptr, w->n);
+    args.np = 1;
+    const int bm = bm_class(m);
+    choose_split_k(args, bm, partial);
+    return hip_status(launch_mfma(args, bm, s), "kr_q4_linear_ws");
+}
+
 int kr_q4_mlp(const kr_q4_matrix *gate, const kr_q4_matrix *up, const kr_q4_matrix *down, const uint16_t *x,
               void *h, int h_dtype, uint32_t m, int activation, void *workspace, size_t workspace_bytes,
               void *stream) {

@@ -85,6 +85,8 @@ def lib():
             "kr_q4_to_split": (i32, [M, vp, vp, vp]),
             "kr_f16_to_bf16": (i32, [vp, vp, sz, vp]),
             "kr_q4_linear": (i32, [M, vp, u32, vp, i32, i32, vp]),
+            "kr_q4_linear_workspace_bytes": (sz, [u32, u32, u32]),
+            "kr_q4_linear_ws": (i32, [M, vp, u32, vp, i32, i32, vp, sz, vp]),
             "kr_q4_gate_up_act": (i32, [M, M, vp, u32, vp, i32, i32, vp]),
             "kr_q4_mlp_workspace_bytes": (sz, [u32, u32, u32]),
             "kr_q4_qkv": (i32, [M, M, M, vp, vp, vp, vp, u32, vp, vp, vp, i32, vp]),
@@ -243,13 +245,28 @@ def f16_to_bf16(t: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None
 
 
 def q4_linear(w: Q4Matrix, x: torch.Tensor, y: Optional[torch.Tensor] = None, out_dtype: int = DTYPE_F32,
-              accumulate: bool = False, stream=None) -> torch.Tensor:
-    """y[m, n] (=|+=) x[m, k] @ W^T.  x is bf16 [m, k] (or [k])."""
+              accumulate: bool = False, workspace: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """y[m, n] (=|+=) x[m, k] @ W^T.  x is bf16 [m, k] (or [k]).  With a workspace (linear_workspace),
+    kr_q4_linear_ws: a few tokens over a long K split K over blocks."""
     m = x.numel() // w.k
     if y is None:
         y = torch.zeros((m, w.n), dtype=_out_dtype(out_dtype), device=x.device)
-    _check(lib().kr_q4_linear(w.desc, _ptr(x), m, _ptr(y), _dt_of(y), int(accumulate), _stream(stream)))
+    if workspace is None:
+        _check(lib().kr_q4_linear(w.desc, _ptr(x), m, _ptr(y), _dt_of(y), int(accumulate), _stream(stream)))
+    else:
+        _check(lib().kr_q4_linear_ws(w.desc, _ptr(x), m, _ptr(y), _dt_of(y), int(accumulate), _ptr(workspace),
+                                     workspace.numel(), _stream(stream)))
     return y
+
+
+def linear_workspace_bytes(m: int, n: int, k: int) -> int:
+    return int(lib().kr_q4_linear_workspace_bytes(m, n, k))
+
+
+def linear_workspace(m: int, n: int, k: int, device="cuda") -> torch.Tensor:
+    """Device workspace of kr_q4_linear_ws (split-K partials and the counters, which must start at zero: the
+    call leaves them zero)."""
+    return torch.zeros(max(linear_workspace_bytes(m, n, k), 16), dtype=torch.uint8, device=device)
 
 
 def gate_up_act(gate: Q4Matrix, up: Q4Matrix, x: torch.Tensor, out: Optional[torch.Tensor] = None,

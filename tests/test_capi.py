@@ -110,6 +110,28 @@ def test_argmax_workspace_sizes_and_checks(kq):
     assert L.kr_argmax_ws(logits, 0, 151936, out, None, 0, None) == 0
 
 
+def test_linear_workspace_sizes_and_checks(kq):
+    """kr_q4_linear_ws: no workspace at m <= 1; otherwise the ticket words then the split-K partials, growing
+    with m (a workspace sized for m serves smaller m); short, missing and misaligned workspaces are refused
+    before anything runs."""
+    L = kq.lib()
+    assert L.kr_q4_linear_workspace_bytes(1, 2048, 11008) == 0
+    sizes = [L.kr_q4_linear_workspace_bytes(m, 2048, 11008) for m in (2, 5, 16, 63, 96)]
+    assert all(sz % 256 == 0 and sz > 0 for sz in sizes) and sizes == sorted(sizes)
+    w = ctypes.byref(_mat(kq, n=2048, k=11008))
+    x, y = 0x40000, 0x50000
+    need = L.kr_q4_linear_workspace_bytes(16, 2048, 11008)
+    assert L.kr_q4_linear_ws(w, x, 16, y, kq.DTYPE_F32, 0, 0x60000, need - 1, None) == kq.KR_E_WORKSPACE
+    assert L.kr_q4_linear_ws(w, x, 16, y, kq.DTYPE_F32, 0, None, need, None) == kq.KR_E_WORKSPACE
+    assert L.kr_q4_linear_ws(w, x, 16, y, kq.DTYPE_F32, 0, 0x60008, need, None) == kq.KR_E_ALIGN
+    assert L.kr_q4_linear_ws(w, x, 16, y, 7, 0, 0x60000, need, None) == kq.KR_E_INVALID
+    assert L.kr_q4_linear_ws(w, x, 16, y, kq.DTYPE_F32, 2, 0x60000, need, None) == kq.KR_E_INVALID
+    assert L.kr_q4_linear_ws(w, None, 16, y, kq.DTYPE_F32, 0, 0x60000, need, None) == kq.KR_E_INVALID
+    assert L.kr_q4_linear_ws(ctypes.byref(_mat(kq, k=96)), x, 16, y, kq.DTYPE_F32, 0, 0x60000, need, None) == \
+        kq.KR_E_SHAPE
+    assert L.kr_q4_linear_ws(w, x, 0, y, kq.DTYPE_F32, 0, None, 0, None) == kq.KR_OK
+
+
 def test_format_argument_checks(kq):
     L = kq.lib()
     assert L.kr_q4_from_blocks36(0x1000, 4, 100, 0x2000, 0x3000, 0x4000, None) == kq.KR_E_SHAPE

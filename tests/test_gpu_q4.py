@@ -313,6 +313,37 @@ def test_linear_few_tokens_long_k(kq, m, n, k):
     assert_bf16_rounded_close(host_bits(accb), O.bf16_to_f32(base_b) + want, rms(want), what=f"m={m} acc bf16")
 
 
+WS_BIG = {}
+
+
+@pytest.mark.parametrize("m", [2, 5, 16, 17, 40, 63, 64, 96])
+@pytest.mark.parametrize("n,k", [(2048, 11008), (300, 4160), (2048, 2752), (96, 2112)])
+def test_linear_ws_long_k(kq, m, n, k):
+    """kr_q4_linear_ws: the same linear with a caller workspace, so that K splits over blocks (the
+    few-token kernel's in-launch reduction at 5 <= m <= 63, the tiled kernel's split and reduction launch
+    at m >= 64).  f32 and bf16-accumulate outputs against the oracle, the same bits on a second call,
+    the workspace's counters left at zero, and one workspace sized for 96 rows serving every m."""
+    s = synth()
+    case(f"linear with workspace m={m} n={n} k={k}")
+    wq = s.q4_weight(n, k, 180 + m + n)
+    x = s.bf16_normal((m, k), 190 + m)
+    want = O.q4_matmul(O.Q4Planar(*wq), x)
+    wd, xd = q4_dev(kq, wq), dev_bf16(x)
+    ws = kq.linear_workspace(m, n, k)
+    y = kq.q4_linear(wd, xd, out_dtype=kq.DTYPE_F32, workspace=ws)
+    assert_rms_close(y.cpu().numpy(), want, what=f"m={m} f32")
+    assert int(torch.count_nonzero(ws[:2048])) == 0
+    y2 = kq.q4_linear(wd, xd, out_dtype=kq.DTYPE_F32, workspace=ws)
+    assert torch.equal(y2.view(torch.int32), y.view(torch.int32))
+    if (n, k) not in WS_BIG:
+        WS_BIG[(n, k)] = kq.linear_workspace(96, n, k)
+    base_b = s.bf16_normal((m, n), 200 + m)
+    accb = dev_bf16(base_b).clone()
+    kq.q4_linear(wd, xd, y=accb, accumulate=True, workspace=WS_BIG[(n, k)])
+    assert_bf16_rounded_close(host_bits(accb), O.bf16_to_f32(base_b) + want, rms(want), what=f"m={m} acc bf16")
+    assert int(torch.count_nonzero(WS_BIG[(n, k)][:2048])) == 0
+
+
 @pytest.mark.parametrize("m", [2, 3, 4])
 @pytest.mark.parametrize("n,k", [(500, 2048), (37, 1408), (11008, 2048)])
 def test_gemv_tokens_gate_up(kq, m, n, k):
