@@ -568,3 +568,35 @@ def test_mlp_graph_replays(kq):
         graph.replay()
         torch.cuda.synchronize()
         assert np.array_equal(h.cpu().numpy().view(np.uint32), eager.view(np.uint32)), f"replay {i}"
+
+
+@pytest.mark.parametrize("m", [16, 96])
+def test_linear_ws_graph_replays(kq, m):
+    """kr_q4_linear_ws captured in a HIP graph (the split-K partials and counters in the workspace):
+    3 replays, with eager work on the same workspace between them, each giving the eager bits."""
+    s = synth()
+    case(f"linear_ws m={m} in a HIP graph, 3 replays vs eager")
+    n, k = 2048, 11008
+    wq = s.q4_weight(n, k, 1003)
+    x = dev_bf16(s.bf16_normal((m, k), 1020 + m))
+    W = q4_dev(kq, wq)
+    ws = kq.linear_workspace(m, n, k)
+    y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    kq.q4_linear(W, x, y=y, workspace=ws)
+    eager = y.cpu().numpy().copy()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            kq.q4_linear(W, x, y=y, workspace=ws)
+    torch.cuda.synchronize()
+    for i in range(3):
+        y.zero_()
+        other = kq.q4_linear(W, x, out_dtype=kq.DTYPE_F32, workspace=ws)  # eager use of the workspace
+        torch.cuda.synchronize()
+        assert np.array_equal(other.cpu().numpy().view(np.uint32), eager.view(np.uint32))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), eager.view(np.uint32)), f"replay {i}"
+        assert int(torch.count_nonzero(ws[:2048])) == 0
