@@ -15,12 +15,14 @@
 //     instruction reads 1 KiB of a row contiguously).  Waves are persistent:
 //     the x operand pairs of the lane's chunks are built once, and the next
 //     tile's weights are loaded while the current tile is reduced.
-//   * long-row kernel, 4096 < k <= 16384 (the down projection, k = 11008):
-//     one 1024-thread block per RB rows; thread (g, c) requests chunk c of
-//     its row group's RB/2 rows at once and builds the x pairs of chunk c
-//     once for all of them, so x is read once per RB rows (the split-K block
-//     kernel reads it once per R = 2 rows: 22 KB per 12 KB of weights).
-//   * block kernel (split-K), longer rows or when a split-K threshold is set:
+//   * long-row kernel, 4096 < k <= 24576 (the down projection, k = 11008):
+//     one block per RB rows (4 by default) with a wave per 64 chunks of the
+//     row (512 threads up to k = 16384, 768 beyond); thread c
+//     requests chunk c of all the block's rows at once and builds the x pairs
+//     of chunk c once for all of them, so x is read once per RB rows (the
+//     split-K block kernel reads it once per R = 2 rows: 22 KB per 12 KB of
+//     weights).
+//   * block kernel (split-K), the gate/up pairs over k > 4096, or any rows when a split-K threshold is set:
 //     the 256 threads of a block share the chunks of R rows; thread i reads
 //     chunks i, i+256, i+512; the four wave partials are added through LDS.
 //
@@ -139,25 +141,27 @@ __global__ __launch_bounds__(256) void q4_gemv_block_kernel(Q4Mat A, Q4Mat B, co
 // ---------------------------------------------------------------- long-row kernel
 
 // Rows longer than the wave kernel covers (the down projection, k = 11008), up
-// to 512 chunks: one 1024-thread block per RB rows.  Thread (g, c) with row
-// group g = wave / 8 (rows g, g + 2, ..., of the block) and chunk c = 64 (wave
-// mod 8) + lane requests the chunk c of all its rows at once, builds the x
-// pairs of chunk c once and reuses them for those rows -- x is read once per
-// block, not once per row pair -- then the rows are reduced in a fixed order
-// (butterfly, then the 8 waves of the group in order).
+// to 64 W chunks: one block of NG row groups of W waves per RB rows (W = 8: up to
+// 512 chunks, k <= 16384; W = 12, one row group, up to 768 chunks: k <= 24576,
+// the largest k the library takes).  Thread (g, c) with row group g = wave / W (rows g,
+// g + NG, ..., of the block) and chunk c = 64 (wave mod W) + lane requests the
+// chunk c of all its rows at once, builds the x pairs of chunk c once and
+// reuses them for those rows -- x is read once per block, not once per row
+// pair -- then the rows are reduced in a fixed order (butterfly, then the W
+// waves of the group in order).
 // M > 1: x holds M token rows; thread (g, c) multiplies its words with the
 // chunk c of every token and the block stores M rows of outputs.
-template <int RB, int EPI, int M = 1, int NG = 2>
-__global__ __launch_bounds__(NG * 512) void q4_gemv_rows_kernel(Q4Mat A, const uint16_t *__restrict__ x, GemvOut o) {
+template <int RB, int EPI, int M = 1, int NG = 2, int W = 8>
+__global__ __launch_bounds__(NG * W * 64) void q4_gemv_rows_kernel(Q4Mat A, const uint16_t *__restrict__ x, GemvOut o) {
     constexpr int RPG = RB / NG;
     constexpr int MP = tokens_pow2<M>();
     constexpr int kVals = RPG * MP;  // values per thread: (row i of the group, token), tokens padded
     constexpr int kSeg = kWave / kVals;
-    __shared__ float red[NG][8][kVals];
+    __shared__ float red[NG][W][kVals];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const uint32_t g = NG == 1 ? 0u : wave >> 3, c = (wave & 7) * kWave + lane;
+    const uint32_t g = NG == 1 ? 0u : wave / W, c = (wave % W) * kWave + lane;
     const uint32_t r0 = blockIdx.x * RB;
     const uint32_t nchunks = A.k >> 5, wpr = A.k >> 3, groups = A.k >> 6;
     const uint32_t kMask = sgpr_const(0x000F000Fu);
@@ -196,14 +200,14 @@ __global__ __launch_bounds__(NG * 512) void q4_gemv_rows_kernel(Q4Mat A, const u
         for (int i = 0; i < RPG; ++i) chunk_dot_m<M>(wv[i], sv[i], bv[i], xc, acc, i * MP, kMask, kMagic);
     }
     const float tot = wave_reduce_vec<kVals>(acc, lane);
-    if ((lane % kSeg) == 0) red[g][wave & 7][lane / kSeg] = tot;
+    if ((lane % kSeg) == 0) red[g][wave % W][lane / kSeg] = tot;
     __syncthreads();
     if (tid < RB * M && out_row < A.n) {
         const uint32_t rr = (uint32_t)tid % RB;
         const uint32_t gg = rr % NG, v = (rr / NG) * MP + out_tok;
         float sum = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 8; ++w) sum += red[gg][w][v];
+        for (int w = 0; w < W; ++w) sum += red[gg][w][v];
         store_row<EPI>(o, out_idx, sum, pre);
     }
 }
@@ -294,11 +298,17 @@ static hipError_t launch_epi(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, 
     const uint32_t chunks = a.k >> 5;
     const int lr = tuning().gemv_long_rows;
     if constexpr (!kGateUp) {
-        if (lr > 0 && chunks > 128 && chunks <= 512 && tuning().gemv_split_k_chunks == 0) {
+        if (lr > 0 && chunks > 128 && chunks <= 768 && tuning().gemv_split_k_chunks == 0) {
             const uint32_t blocks = (a.n + lr - 1) / lr;
 #define KR_ROWS(RB, NG) \
     hipLaunchKernelGGL((q4_gemv_rows_kernel<RB, EPI, 1, NG>), dim3(blocks), dim3(NG * 512), 0, s, a, x, o)
-            if (tuning().gemv_long_groups == 1) {
+#define KR_ROWS_W(RB, W) \
+    hipLaunchKernelGGL((q4_gemv_rows_kernel<RB, EPI, 1, 1, W>), dim3(blocks), dim3(W * 64), 0, s, a, x, o)
+            if (chunks > 512) {  // 16384 < k <= kMaxGemvK: 12 waves per row group, one group
+                if (lr == 4) KR_ROWS_W(4, 12);
+                else if (lr == 16) KR_ROWS_W(16, 12);
+                else KR_ROWS_W(8, 12);
+            } else if (tuning().gemv_long_groups == 1) {
                 if (lr == 4) KR_ROWS(4, 1);
                 else if (lr == 16) KR_ROWS(16, 1);
                 else KR_ROWS(8, 1);
@@ -308,6 +318,7 @@ static hipError_t launch_epi(const Q4Mat &a, const Q4Mat &b, const uint16_t *x, 
                 else KR_ROWS(8, 2);
             }
 #undef KR_ROWS
+#undef KR_ROWS_W
             return hipGetLastError();
         }
     }

@@ -158,9 +158,9 @@ def test_gemv_shapes(kq, n, k):
         assert_rms_close(y, want, what=f"n={n} k={k} rows/wave={rpw}")
 
 
-@pytest.mark.parametrize("n,k", [(37, 4160), (2048, 11008), (100, 16384)])
+@pytest.mark.parametrize("n,k", [(37, 4160), (2048, 11008), (100, 16384), (40, 16448), (300, 18944), (33, 24576)])
 def test_gemv_long_row_kernel_options(kq, n, k):
-    """The long-row kernel (4096 < k <= 16384) at every rows-per-block / row-group setting: each matches the
+    """The long-row kernel (4096 < k <= 24576; 12 waves per block beyond 16384) at every rows-per-block / row-group setting: each matches the
     oracle, and all give the same bits (one chunk per lane and a fixed reduction order in every setting)."""
     s = synth()
     case(f"gemv long rows n={n} k={k}, rows per block 4/8/16 x row groups 1/2")
@@ -181,6 +181,34 @@ def test_gemv_long_row_kernel_options(kq, n, k):
     for key, y in outs.items():
         assert_rms_close(y, want, what=f"groups={key[0]} rows={key[1]}")
         assert np.array_equal(y.view(np.uint32), outs[(1, 4)].view(np.uint32)), key
+
+
+@pytest.mark.parametrize("epi", ["f32", "bf16", "acc_f32", "acc_bf16"])
+def test_gemv_longest_rows_epilogues(kq, epi):
+    """m = 1 over k = 18944 (a 7B-class down projection, 592 chunks: the 12-wave long-row blocks) with every
+    epilogue, against the oracle."""
+    s = synth()
+    n, k = 3584, 18944
+    case(f"gemv n={n} k={k} epilogue {epi}")
+    wq = s.q4_weight(n, k, 610)
+    x = s.bf16_normal((1, k), 611)
+    want = O.q4_matmul(O.Q4Planar(*wq), x)
+    w, xd = q4_dev(kq, wq), dev_bf16(x)
+    if epi == "f32":
+        assert_rms_close(kq.q4_linear(w, xd, out_dtype=kq.DTYPE_F32).cpu().numpy(), want, what=epi)
+    elif epi == "bf16":
+        yb = kq.q4_linear(w, xd, out_dtype=kq.DTYPE_BF16)
+        assert_bf16_rounded_close(host_bits(yb), want, rms(want), what=epi)
+    elif epi == "acc_f32":
+        base = s.f32_normal((1, n), 612)
+        acc = torch.from_numpy(base.copy()).cuda()
+        kq.q4_linear(w, xd, y=acc, accumulate=True)
+        assert_rms_close(acc.cpu().numpy() - base, want, what=epi)
+    else:
+        base_b = s.bf16_normal((1, n), 613)
+        acc = dev_bf16(base_b).clone()
+        kq.q4_linear(w, xd, y=acc, accumulate=True)
+        assert_bf16_rounded_close(host_bits(acc), O.bf16_to_f32(base_b) + want, rms(want), what=epi)
 
 
 def test_stream_read_reads_every_piece(kq):
