@@ -20,7 +20,7 @@ def rms(a) -> float:
 
 
 def assert_rms_close(got, want, rel=1e-2, what=""):
-    """The north-star bar: max |got - want| <= rel * RMS(want)."""
+    """The parity bar for floating-point outputs: max |got - want| <= rel * RMS(want)."""
     got = np.asarray(got, dtype=np.float64)
     want = np.asarray(want, dtype=np.float64)
     assert got.shape == want.shape, (got.shape, want.shape)

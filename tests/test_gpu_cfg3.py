@@ -9,7 +9,7 @@ encoder.rs:4880-5516).
 Bars:
 - the LM head (kr_q4_linear at N = 151936) and the fused-norm few-token calls
   at H = 2048: max |gpu - oracle| <= 1e-2 * RMS(oracle) per matmul;
-- decode logits: max |gpu - cpu| <= 1e-2 * RMS(cpu), the north-star bar of
+- decode logits: max |gpu - cpu| <= 1e-2 * RMS(cpu), the parity bar of
   one matmul, held by the whole step (measured 0.9-2.0e-3 at 2 and 36 layers:
   the device and the restatement round to bf16 at the same points, so only
   the f32 summation order differs, and a value rounded the other way moves by

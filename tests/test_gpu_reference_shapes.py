@@ -15,7 +15,7 @@ their inputs, through the C ABI:
     rows, within the bar.
 
 Bars: the reference's own (|d| > 0.05 and rel > 0.05 fails for the GEMV; a mismatch rate below 1 %
-for the prefill GEMM) and the north-star bar max |gpu - oracle| <= 1e-2 RMS(oracle), bf16 outputs
+for the prefill GEMM) and the parity bar max |gpu - oracle| <= 1e-2 RMS(oracle), bf16 outputs
 the RNE of a value within it."""
 import math
 
